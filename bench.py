@@ -1,0 +1,313 @@
+#!/usr/bin/env python3
+"""Benchmark of the static INT8 KV-cache hot path on one MI355X.
+
+Headline (BASELINE.json metric, config c2): INT8 paged decode attention, 128 requests x 32768 keys,
+28 q / 4 kv heads, head_dim 128, block 16, in vLLM's interleaved [nb, H, bs, 2D] int8 cache (filled
+with c0-distribution codes by this package's quantize-and-cache kernel), shuffled block tables over
+263,168 blocks. A step is one kvq.cuda_kernels.decode_attention call (attention kernel + split merge)
+with every input resident in HBM.
+
+Prints ONE JSON line. `value` is algorithmic bytes / step time (GB/s); `roofline` times the attention
+kernel alone with HIP events recorded around it on its own stream; `cpu_baseline` times the CPU oracle
+(the reference's implementation B + run_paged restated) on a bounded sample of the same requests and
+checks the GPU output of those requests against it. `extra` carries configs c1 (fused quantize +
+cache write), c3 (8-token verification) and c4 (Llama-3 mixed batch: decode rows + page dequant).
+
+  python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "int8-kvcache_amd"))
+
+import torch  # noqa: E402
+
+from kvq import _native, synth  # noqa: E402
+from kvq import cuda_kernels as ck  # noqa: E402
+
+with open(os.path.join(REPO, "BASELINE.json")) as _f:
+    METRIC = json.load(_f)["metric"]
+PEAK_GBS = 8000.0          # MI355X HBM3E
+PEAK_INT8_OPS = 5.0e15     # dense int8 MFMA
+DEV = "cuda"
+
+
+# ------------------------------------------------------------------------------------------------ HIP events
+class HipEvents:
+    """Raw hipEvent_t pairs (the library records them on the stream it launches on)."""
+
+    def __init__(self, n):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.pairs = []
+        for _ in range(n):
+            a, b = ctypes.c_void_p(), ctypes.c_void_p()
+            assert self.hip.hipEventCreate(ctypes.byref(a)) == 0 and self.hip.hipEventCreate(ctypes.byref(b)) == 0
+            self.pairs.append((a, b))
+
+    def elapsed_ms(self, i):
+        ms = ctypes.c_float()
+        a, b = self.pairs[i]
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def close(self):
+        for a, b in self.pairs:
+            self.hip.hipEventDestroy(a)
+            self.hip.hipEventDestroy(b)
+
+
+def interleaved_cache(nb, hkv, bs, d):
+    """vLLM's int8 layout [nb, H, bs, 2D] and its K / V views [nb, bs, H, D] (backend.py:145-147)."""
+    kv = torch.empty(nb, hkv, bs, 2 * d, dtype=torch.int8, device=DEV)
+    kc, vc = kv.transpose(1, 2).split(d, dim=-1)
+    return kv, kc, vc
+
+
+# ------------------------------------------------------------------------------------------------ c2 headline
+def build_c2(B=128, L=32768, hq=28, hkv=4, d=128, bs=16):
+    pages = L // bs
+    nb = B * pages + 1024
+    params = synth.channel_params(hkv, d)
+    st = {k: v.to(DEV) for k, v in synth.calibration_scales(hkv, d, params).items()}
+    kv, kc, vc = interleaved_cache(nb, hkv, bs, d)
+    synth.fill_cache_gpu(kc, vc, st, params, seed=3, write=ck.quant_reshape_and_cache)
+    bt = synth.random_block_table(B, [pages] * B, nb, 4, DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q = torch.randn(B, hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=DEV)
+    sl = torch.full((B,), L, dtype=torch.int32, device=DEV)
+    alg = (B * L * hkv * d * 2 + 2 * B * hq * d * 2 + B * pages * 4 + (2 * B + 1) * 4 + 2 * hkv * d * 4)
+    return {"q": q, "kc": kc, "vc": vc, "kv": kv, "cu": cu, "sl": sl, "bt": bt, "st": st, "B": B, "L": L,
+            "hq": hq, "hkv": hkv, "d": d, "bs": bs, "alg_bytes": alg, "kv_bytes": B * L * hkv * d * 2}
+
+
+def time_c2(w, steps, warmup):
+    out = torch.empty_like(w["q"])
+    scale = w["d"] ** -0.5
+
+    def step():
+        ck.decode_attention(w["q"], w["kc"], w["vc"], out, w["cu"], w["sl"], w["bt"], scale, w["st"])
+
+    for _ in range(warmup):
+        step()
+    ev = HipEvents(steps)
+    lib = _native.load()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        a, b = ev.pairs[i]
+        lib.kvq_set_attention_events(a, b)
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kern_ms = [ev.elapsed_ms(i) for i in range(steps)]
+    ev.close()
+    splits = ck.choose_splits(w["B"], w["hkv"], w["hq"], 1, w["bt"].shape[1] * w["bs"],
+                              torch.cuda.get_device_properties(0).multi_processor_count)
+    return out, (t1 - t0) * 1e3 / steps, statistics.mean(kern_ms), statistics.median(kern_ms), splits
+
+
+# ------------------------------------------------------------------------------------------------ CPU baseline
+def cpu_baseline(w, out, budget_s=12.0, max_reqs=32):
+    """The CPU oracle (port of int8_ref B + run_paged) on whole c2 requests until ~budget_s of CPU work;
+    also the parity of the GPU output on those requests."""
+    sys.path.insert(0, REPO)
+    from oracle import kvq_oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    st = {k: v.cpu() for k, v in w["st"].items()}
+    f = O.paged_static_attention(O.CFG32_Q32, st, True, 8)
+    pages = w["L"] // w["bs"]
+    t_total, n, errs, kv_bytes = 0.0, 0, [], 0
+    one = torch.tensor([0, 1], dtype=torch.int32)
+    while n < max_reqs and t_total < budget_s:
+        r = (n * 37) % w["B"]
+        ids = w["bt"][r, :pages].long()
+        kq, vq = w["kc"][ids].cpu(), w["vc"][ids].cpu()
+        q = w["q"][r:r + 1].cpu()
+        bt = torch.arange(pages, dtype=torch.int32)[None]
+        sl = torch.tensor([w["L"]], dtype=torch.int32)
+        t0 = time.perf_counter()
+        ref = f(q.float(), kq, vq, one, sl, bt, w["d"] ** -0.5)
+        t_total += time.perf_counter() - t0
+        kv_bytes += w["L"] * w["hkv"] * w["d"] * 2
+        e = O.compare(ref, out[r:r + 1].cpu())
+        errs.append(e)
+        n += 1
+    parity = {"requests_checked": n, "max_abs": max(e["max_abs"] for e in errs),
+              "mean_abs": statistics.mean(e["mean_abs"] for e in errs),
+              "rel_l2_max": max(e["rel_l2"] for e in errs), "bar": "max_abs<=2e-2, mean_abs<=2e-3"}
+    parity["ok"] = parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3
+    return {"value": round(kv_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} whole c2 requests (32768 keys, 28/4/128) through the oracle's implementation B "
+                      f"(float64) + run_paged on the host, {t_total:.1f} s; KV bytes / s",
+            "us_per_request": round(t_total / n * 1e6, 1)}, parity
+
+
+# ------------------------------------------------------------------------------------------------ extras
+def _median_event_ms(fn, reps, rotate):
+    """Median over `reps` calls, each on the next of `rotate` buffer sets, timed with torch events
+    on the current stream (the stream the kernels are launched on)."""
+    for i in range(min(5, reps)):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i % rotate)
+        b.record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
+
+
+def bench_c1(reps=200):
+    """Fused quantize + cache write, 16384 tokens x 4 x 128, ~2% padding, 4096 x 16 interleaved cache.
+    4 distinct input/cache sets (~400 MB) are rotated to defeat the 256 MB last-level cache."""
+    sets = []
+    for s in range(4):
+        c = synth.c1_inputs(seed=5 + s)
+        kv, kc, vc = interleaved_cache(c["num_blocks"], 4, c["block_size"], 128)
+        sets.append((c["key"].to(DEV), c["value"].to(DEV), kc, vc, c["slots"].to(DEV),
+                     {k: v.to(DEV) for k, v in c["static"].items()}))
+    T = sets[0][0].shape[0]
+    t_valid = int((sets[0][4] >= 0).sum())
+    alg = t_valid * 3072 + T * 8 + 6144
+
+    def fn(i):
+        k, v, kc, vc, sl, st = sets[i]
+        ck.quant_reshape_and_cache(k, v, kc, vc, sl, st)
+
+    ms = _median_event_ms(fn, reps, len(sets))
+    return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
+            "alg_bytes": alg, "tokens": T, "valid": t_valid}
+
+
+def bench_c3(reps=200):
+    """64 requests x 8 query tokens (causal), L log-uniform in [512, 8192], 28/4/128: two cache copies
+    (~360 MB) rotated."""
+    lens = synth.c3_lens()
+    hq, hkv, d, bs = 28, 4, 128, 16
+    pages = [-(-L // bs) for L in lens]
+    nb = sum(pages) + 64
+    params = synth.channel_params(hkv, d)
+    st = {k: v.to(DEV) for k, v in synth.calibration_scales(hkv, d, params).items()}
+    sets = []
+    for s in range(2):
+        kv, kc, vc = interleaved_cache(nb, hkv, bs, d)
+        synth.fill_cache_gpu(kc, vc, st, params, seed=30 + s, write=ck.quant_reshape_and_cache)
+        sets.append((kc, vc, synth.random_block_table(64, pages, nb, 40 + s, DEV)))
+    g = torch.Generator(device=DEV).manual_seed(6)
+    q = torch.randn(64 * 8, hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    cu = torch.arange(65, dtype=torch.int32, device=DEV) * 8
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(q)
+
+    def fn(i):
+        kc, vc, bt = sets[i]
+        ck.decode_attention(q, kc, vc, out, cu, sl, bt, d ** -0.5, st, max_query_len=8)
+
+    ms = _median_event_ms(fn, reps, len(sets))
+    kvb = sum(lens) * hkv * d * 2
+    alg = kvb + 2 * q.numel() * 2 + sum(pages) * 4 + 129 * 4 + 2 * hkv * d * 4
+    ops = sum(lens) * hkv * 28672
+    return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
+            "alg_bytes": alg, "useful_int8_ops": ops, "mfma_util": round(ops / (ms * 1e-3) / PEAK_INT8_OPS, 5)}
+
+
+def bench_c4(reps=50):
+    """Llama-3 heads (32 / 8, d128): 96 decode rows (L log-uniform in [1, 32768]) through the INT8
+    kernel, and the 4 x 16384-token prefill requests' pages dequantized to bf16 (dequant_pages)."""
+    lens = synth.c4_lens()
+    hq, hkv, d, bs = 32, 8, 128, 16
+    pre = [16384] * 4
+    dec_pages = [-(-L // bs) for L in lens]
+    pre_pages = [L // bs for L in pre]
+    nb = sum(dec_pages) + sum(pre_pages) + 64
+    params = synth.channel_params(hkv, d)
+    st = {k: v.to(DEV) for k, v in synth.calibration_scales(hkv, d, params).items()}
+    kv, kc, vc = interleaved_cache(nb, hkv, bs, d)
+    synth.fill_cache_gpu(kc, vc, st, params, seed=50, write=ck.quant_reshape_and_cache)
+    bt = synth.random_block_table(100, dec_pages + pre_pages, nb, 51, DEV)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    q = torch.randn(96, hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    cu = torch.arange(97, dtype=torch.int32, device=DEV)
+    sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(q)
+    ms_dec = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st), reps, 1)
+    cu_all = torch.tensor([0] + [int(x) for x in torch.cumsum(torch.tensor([1] * 96 + pre), 0)], dtype=torch.int32)
+    plan = ck.plan_long(cu_all, torch.tensor(lens + pre), bs)
+    src_req, src_j, _ = plan.gpu(DEV)
+    P = src_req.shape[0]
+    ko = torch.empty(P, bs, hkv, d, dtype=torch.bfloat16, device=DEV)
+    vo = torch.empty_like(ko)
+    ms_dq = _median_event_ms(lambda i: ck.ext().dequant_pages(kc, vc, ko, vo, bt, src_req, src_j, st["k_scale"],
+                                                              st["v_scale"]), reps, 1)
+    dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
+    dq_alg = P * bs * hkv * d * 2 * (1 + 2) + P * 12
+    return {"decode_us": round(ms_dec * 1e3, 2), "decode_GBps": round(dec_alg / ms_dec / 1e6, 1),
+            "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4),
+            "dequant_us": round(ms_dq * 1e3, 2), "dequant_GBps": round(dq_alg / ms_dq / 1e6, 1),
+            "dequant_frac": round(dq_alg / ms_dq / 1e6 / PEAK_GBS, 4), "dequant_pages": P,
+            "note": "bf16 prefill attention consumer not timed (torch fp32 stand-in for FlashAttention)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this path has no multi-GPU mode (every kernel shards per request / "
+              "kv head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    torch.cuda.set_device(0)
+    ck.ext()
+    print("# building c2 workload", file=sys.stderr, flush=True)
+    w = build_c2()
+    torch.cuda.synchronize()
+    print("# timing c2", file=sys.stderr, flush=True)
+    out, ms_step, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup)
+    alg = w["alg_bytes"]
+    res = {
+        "metric": METRIC,
+        "value": round(alg / (ms_step * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "us_per_call": round(ms_step * 1e3, 1),
+        "kv_GBps": round(w["kv_bytes"] / (ms_step * 1e-3) / 1e9, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 (int32 MFMA accumulate, fp32 softmax, bf16 out)",
+        "data": "synthetic (c0 distribution, seeded)",
+        "config": {"workload": "c2: INT8 paged decode attention, 128 requests x 32768 keys, 28 q / 4 kv heads, "
+                               "d128, block 16, vLLM interleaved int8 cache, shuffled block tables",
+                   "splits": splits, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(alg / (kern_ms_mean * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / (kern_ms_mean * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_kernel<128,1>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
+                     "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
+    }
+    if not args.no_cpu:
+        print("# cpu baseline", file=sys.stderr, flush=True)
+        res["cpu_baseline"], res["parity"] = cpu_baseline(w, out)
+    del w
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        print("# extras", file=sys.stderr, flush=True)
+        res["extra"] = {"c1_quant_cache": bench_c1(), "c3_verify_8tok": bench_c3(), "c4_llama3_mixed": bench_c4()}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

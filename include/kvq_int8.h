@@ -1,0 +1,108 @@
+/* C ABI of the MI355X (gfx950) static INT8 KV-cache kernels.
+ *
+ * Every entry point takes plain device pointers, element strides (int64) and a hipStream_t passed
+ * as void*. Nothing here allocates device memory or synchronises the host: each call validates its
+ * arguments, enqueues its kernels on `stream` and returns 0, or returns a nonzero KVQ_ERR_* code
+ * without launching anything; kvq_last_error() then describes the failure (thread-local string).
+ *
+ * Layout conventions (all strides in elements of the pointed-to type):
+ *   key/value      bf16  [T, H, D]       strides (st, sh, 1)
+ *   k/v cache      int8  [nb, bs, H, D]  strides (sb, sn, sh, 1) -- vLLM's interleaved
+ *                                         [nb, H, bs, 2D] view or separate caches alike
+ *   q / out        bf16  [T, Hq, D]      strides (st, sh, 1)
+ *   slot_mapping   int64 [n], -1 = padding (skipped)
+ *   cu_seqlens_q   int32 [B + 1], seq_lens int32 [B], block_table int32 [B, W] (row stride)
+ *   k/v scales     fp32  [Hkv, D] (per channel) or [Hkv, 1] (per head), contiguous; k_mu fp32 [Hkv, D]
+ * head_dim D is 64 or 128; block_size a power of two >= 16. Base pointers of bf16 / int8 rows must be
+ * 16-byte aligned and their row strides multiples of 16 bytes (vLLM's views satisfy this).
+ * Page ids read from a block table outside [0, num_blocks) are replaced by page 0 inside the kernels,
+ * so a malformed table yields garbage rows rather than a memory fault (the reference leaves this
+ * undefined; its KVQ_DEBUG host check, mirrored in kvq/cuda_kernels.py, reports such tables).
+ */
+#ifndef KVQ_INT8_H
+#define KVQ_INT8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  KVQ_OK = 0,
+  KVQ_ERR_ARG = 1,     /* shape / layout / value rejected before launch */
+  KVQ_ERR_LAUNCH = 2,  /* the HIP runtime reported an error for the launch */
+};
+
+/* Fused quantize + reshape_and_cache.
+ * Replaces the pybind op quant_cache (reference kvq/cuda/int8_kv.cu:554-575, kernel :55-84), bound
+ * as kvq/cuda_kernels.py:42-44 quant_reshape_and_cache.
+ *   kc[slot / bs, slot % bs, h, d] = sat127(rint(fl((f32(key[t,h,d]) - k_mu[h,d]) / k_scale)))
+ *   vc[...]                        = sat127(rint(fl(f32(value[t,h,d]) / v_scale)))
+ * for t < n_tokens whose slot is in [0, num_blocks * block_size); other slots are skipped.
+ * k_scale_cols / v_scale_cols: D (per channel) or 1 (per head). */
+int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
+                    int64_t val_sh, int8_t* k_cache, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh, int8_t* v_cache,
+                    int64_t vc_sb, int64_t vc_sn, int64_t vc_sh, const int64_t* slot_mapping, int64_t n_tokens,
+                    int64_t num_heads, int64_t head_dim, int64_t num_blocks, int64_t block_size,
+                    const float* k_scale, int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                    const float* k_mu, void* stream);
+
+/* Standalone q quantization (k scale folded in).
+ * Replaces the pybind op quant_q (reference kvq/cuda/int8_kv.cu:577-598, kernel :89-111), bound as
+ * kvq/cuda_kernels.py:47-48. x = f32(q[t,h,:]) * k_scale[h / G, :] when k_scale_cols == D (a per-head
+ * K scale is not folded); one scale s = max(amax_group / 127, 1e-8) per `group` channels (128 or 32,
+ * D = 128); q_i8 = sat127(rint(fl(x / s))). Outputs: q_i8 contiguous [T, Hq, 128], q_scale contiguous
+ * [T, Hq, 128 / group]. */
+int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, int64_t num_q_heads,
+                int64_t head_dim, const float* k_scale, int64_t num_kv_heads, int64_t k_scale_cols,
+                int64_t group, int8_t* q_i8, float* q_scale, void* stream);
+
+/* INT8 paged attention for requests with 1 <= q_len <= qmax (decode, spec-decode verification),
+ * implementation B of the reference (kvq/int8_ref.py:108-143 with p_tile = 32).
+ * Replaces the pybind op int8_decode_attention (reference kvq/cuda/int8_kv.cu:600-648, kernels
+ * :168-463 and :472-503), bound as kvq/cuda_kernels.py:51-58 decode_attention.
+ * Requests with q_len == 0 or q_len > qmax are skipped (their out rows untouched).
+ * num_splits == 1: out written directly, segm_* ignored (may be NULL).
+ * num_splits  > 1 (<= 64): the context is split in num_splits ranges of whole 32-key tiles; partials
+ *   go to segm_out [T, Hq, S, D], segm_max / segm_sum [T, Hq, S] (fp32; element (t, h, s) at
+ *   t * seg_st + h * seg_sh + s, segm_out at that index * D + d) and a second kernel merges them. */
+int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                              int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                              int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                              int64_t head_dim, void* out,
+                              int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                              const int32_t* block_table, int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads,
+                              const float* k_scale, int64_t k_scale_cols, const float* v_scale,
+                              int64_t v_scale_cols, double softmax_scale, float* segm_out, float* segm_max,
+                              float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
+                              int64_t max_query_len, int64_t qmax, void* stream);
+
+/* Dequantize pages of the INT8 cache into a contiguous bf16 cache [P, bs, H, D] (long-query path).
+ * Replaces the pybind op dequant_pages (reference kvq/cuda/int8_kv.cu:650-672, kernel :505-542),
+ * called from kvq/cuda_kernels.py:120-122. Output page p is page src_j[p] of request src_req[p]:
+ * physical page block_table[src_req[p] * bt_stride + src_j[p]]. ko = bf16_rne(f32(k_i8) * k_scale)
+ * (K keeps k - mu), vo likewise. */
+int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t k_sh, const int8_t* v_cache,
+                      int64_t v_sb, int64_t v_sn, int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_heads,
+                      int64_t head_dim, void* k_out, void* v_out, const int32_t* block_table, int64_t bt_stride,
+                      const int32_t* src_req, const int32_t* src_j, int64_t num_pages, const float* k_scale,
+                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, void* stream);
+
+/* Instrumentation, no counterpart in the reference: when set (non-NULL hipEvent_t handles), the next
+ * kvq_int8_decode_attention call on this thread records `start` on its stream right before the
+ * attention kernel and `stop` right after it (before the split merge), then forgets the pair. Lets a
+ * benchmark time the attention kernel alone with events. Returns 0. */
+int kvq_set_attention_events(void* start, void* stop);
+
+/* Text of the last error on this thread ("" if none). */
+const char* kvq_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int kvq_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVQ_INT8_H */

@@ -1,0 +1,291 @@
+"""The CPU oracle pinned against the reference's golden vectors, an independent C restatement,
+closed forms, invariants and brute force (no GPU)."""
+import numpy as np
+import pytest
+import torch
+from conftest import record
+
+import cases
+from oracle import c_oracle
+from oracle import kvq_oracle as O
+from kvq import cuda_kernels as ck
+
+
+def _quantized(c):
+    st = c["static"]
+    return O.quantize(c["k"].float() - st["k_mu"], st["k_scale"]), O.quantize(c["v"], st["v_scale"])
+
+
+def _sha(t):
+    import hashlib
+    return hashlib.sha256(t.contiguous().numpy().tobytes()).hexdigest()
+
+
+# ---------------------------------------------------------------- quantization formulas
+def test_quant_codes_match_reference_golden(golden):
+    g, _ = golden
+    x, s = cases.quant_special()
+    assert torch.equal(O.quantize(x, s), g["quant|codes"])
+    assert torch.equal(O.dequantize(g["quant|codes"], s, torch.bfloat16).view(torch.int16),
+                       g["quant|dequant_bf16"].view(torch.int16))
+
+
+def test_quant_closed_form_corner_cases():
+    x = torch.tensor([0.5, 1.5, 2.5, -0.5, -2.5, 127.5, -127.5, 126.5, 1e9, -1e9, 0.0])
+    assert O.quantize(x, torch.ones_like(x)).tolist() == [0, 2, 2, 0, -2, 127, -127, 126, 127, -127, 0]
+    assert O.scale_from_absmax(torch.tensor([0.0, 127.0])).tolist() == [pytest.approx(1e-8), 1.0]
+
+
+def test_c_restatement_matches_torch_oracle():
+    """IEEE fp32 division + rintf in C == torch's division + round, on random data, exact ties
+    (k + 1/2) * s, and values one ulp either side of a tie."""
+    r = np.random.Generator(np.random.PCG64(3))
+    s = r.uniform(1e-3, 3.0, 200000).astype(np.float32)
+    k = r.integers(-130, 130, 200000).astype(np.float32)
+    tie = (k + 0.5).astype(np.float32) * s                 # fp32 product: often not an exact tie
+    up, dn = np.nextafter(tie, np.float32(np.inf)), np.nextafter(tie, np.float32(-np.inf))
+    rnd = (r.standard_normal(200000) * 80).astype(np.float32)
+    x = torch.from_numpy(np.concatenate([tie, up, dn, rnd]))
+    sc = torch.from_numpy(np.concatenate([s, s, s, s]))
+    assert torch.equal(c_oracle.codes(x, sc), O.quantize(x, sc))
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_c_quant_rows_and_dequant_match_torch(per_channel):
+    r = np.random.Generator(np.random.PCG64(4))
+    x = torch.from_numpy((r.standard_normal((300, 4, 128)) * 5).astype(np.float32)).to(torch.bfloat16)
+    st = O_scales = {"k_scale": torch.from_numpy(r.uniform(0.01, 0.2, (4, 128 if per_channel else 1)).astype(np.float32)),
+                     "k_mu": torch.from_numpy(r.standard_normal((4, 128)).astype(np.float32))}
+    codes = c_oracle.quant_rows(x, st["k_mu"], st["k_scale"])
+    assert torch.equal(codes, O.quantize(x.float() - st["k_mu"], st["k_scale"]))
+    deq = c_oracle.dequant(codes, O_scales["k_scale"])
+    assert torch.equal(deq.view(torch.int16), O.dequantize(codes, st["k_scale"], torch.bfloat16).view(torch.int16))
+
+
+@pytest.mark.parametrize("group", [128, 32])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_c_quant_q_matches_torch(group, per_channel):
+    r = np.random.Generator(np.random.PCG64(5))
+    q = torch.from_numpy(r.standard_normal((37, 28, 128)).astype(np.float32)).to(torch.bfloat16)
+    ks = torch.from_numpy((r.random((4, 128 if per_channel else 1)) + 0.01).astype(np.float32))
+    c1, s1 = c_oracle.quant_q(q, ks, group)
+    c2, s2 = O.quant_q_ref(q, ks, group)
+    assert torch.equal(c1, c2) and torch.equal(s1, s2)
+
+
+def test_fp32_q_rows_match_c_restatement():
+    """The oracle's fp32 q path (the kernel contract) equals the C restatement of the fp32 formula."""
+    r = np.random.Generator(np.random.PCG64(6))
+    q = torch.from_numpy(r.standard_normal((5, 28, 128)).astype(np.float32)).to(torch.bfloat16)
+    for ks in (torch.from_numpy((r.random((4, 128)) + 0.01).astype(np.float32)), torch.full((4, 1), 0.3)):
+        qi, sq = O.quant_q_rows(q.reshape(1, 5, 4, 7, 128), ks[None, None], "fp32")
+        ci, cs = c_oracle.quant_q(q, ks, 128)
+        assert torch.equal(qi.reshape(5, 28, 128).to(torch.int8), ci)
+        assert torch.equal(sq.reshape(5, 28).float(), cs[..., 0])
+
+
+def test_fp64_and_fp32_q_differ_only_on_ties():
+    """With per-head K scales bf16 q rows often hit exact rounding ties of 127 x / amax; fp64 and fp32
+    arithmetic may round those differently and nothing else."""
+    r = np.random.Generator(np.random.PCG64(7))
+    q = torch.from_numpy(r.standard_normal((64, 28, 128)).astype(np.float32)).to(torch.bfloat16)
+    ks = torch.full((1, 1, 4, 1), 0.3)
+    a, sa = O.quant_q_rows(q.reshape(1, 64, 4, 7, 128), ks, "fp64")
+    b, sb = O.quant_q_rows(q.reshape(1, 64, 4, 7, 128), ks, "fp32")
+    diff = a != b
+    assert diff.any()                                          # ties do occur
+    exact = q.float().reshape(1, 64, 4, 7, 128).double() * 127 / q.float().abs().amax(-1, keepdim=True).reshape(
+        1, 64, 4, 7, 1).double()
+    frac = (exact - exact.floor() - 0.5).abs()
+    assert (frac[diff] < 1e-6).all() and ((a - b).abs() <= 1).all()
+
+
+# ---------------------------------------------------------------- golden vectors from the reference
+@pytest.mark.parametrize("name", cases.NAMES)
+def test_oracle_matches_reference_golden(golden, name):
+    g, meta = golden
+    c = cases.build(name)
+    m = meta["cases"][name]
+    assert _sha(c["q"].view(torch.int16)) == m["q_sha256"], "case generator drifted from the fixture"
+    kq, vq = _quantized(c)
+    assert _sha(kq) == m["k_codes_sha256"] and _sha(vq) == m["v_codes_sha256"]
+    cfg = O.CFG32 if c["per_channel"] else O.CFG32_HEAD
+    args = (c["cu"], c["seq_lens"], c["block_table"])
+    out = O.paged_static_attention(cfg, c["static"], cache_is_int8=True, short_q=8)(c["q"], kq, vq, *args, c["scale"])
+    rows = cases.stored_rows(name, c["cu"])
+    ref = g[f"{name}|int8_b"]
+    err = O.compare(ref, out[rows])
+    record("oracle_vs_reference_golden", case=name, **err)
+    # same op sequence as the reference: equal up to an occasional last-bit difference of bf16
+    assert err["max_abs"] <= 2 ** -8 * ref.float().abs().max().item() and err["rel_l2"] < 1e-5
+    if f"{name}|bf16_ref" in g:
+        gold = O.paged_attention_ref(c["q"], c["k"], c["v"], *args, c["scale"])
+        e2 = O.compare(g[f"{name}|bf16_ref"], gold[rows])
+        assert e2["rel_l2"] < 1e-5
+
+
+# ---------------------------------------------------------------- invariants of implementation B
+def _dense_case(b=2, R=3, K=70, hkv=2, G=3, D=64, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    qb = torch.randn(b, R, hkv * G, D, generator=gen)
+    k = torch.randn(b, K, hkv, D, generator=gen) * torch.linspace(0.1, 20, D)
+    v = torch.randn(b, K, hkv, D, generator=gen)
+    return qb, k, v
+
+
+@pytest.mark.parametrize("k_gran", ["per_channel", "per_head"])
+def test_impl_b_algebra_is_exact(k_gran):
+    """q and P unquantized: B must equal fp64 attention on dequantized K/V (tests/test_int8_ref.py:20-38)."""
+    qb, k, v = _dense_case()
+    b, K, hkv, D = k.shape
+    gran_dims = (0, 1, 3) if k_gran == "per_head" else (0, 1)
+    ks = O.scale_from_absmax(k.abs().amax(dim=gran_dims, keepdim=True))   # [1, 1, hkv, D|1]
+    vs = O.scale_from_absmax(v.abs().amax(dim=(0, 1), keepdim=True))
+    kq, vq = O.quantize(k, ks), O.quantize(v, vs)
+    mask = torch.ones(b, qb.shape[1], K, dtype=torch.bool)
+    cfg = O.Cfg(k_gran=k_gran, q_gran="none", p_quant="none")
+    out = O.attend_int8(qb, kq, ks, vq, vs, mask, 0.125, cfg)
+    kd, vd = kq.double() * ks.double(), vq.double() * vs.double()
+    qg = qb.double().reshape(b, qb.shape[1], hkv, -1, D)
+    p = torch.softmax(torch.einsum("brhgd,bkhd->bhgrk", qg, kd) * 0.125, -1)
+    ref = torch.einsum("bhgrk,bkhd->brhgd", p, vd).flatten(2, 3)
+    assert O.compare(ref, out)["rel_l2"] < 1e-6
+
+
+def test_one_key_context_returns_dequantized_v():
+    """A single visible key: P = 1 quantizes to 127 and the normalisation cancels -> o = v_i8 * s_v."""
+    qb, k, v = _dense_case(K=1)
+    ks = O.scale_from_absmax(k.abs().amax(dim=(0, 1), keepdim=True))
+    vs = O.scale_from_absmax(v.abs().amax(dim=(0, 1), keepdim=True))
+    kq, vq = O.quantize(k, ks), O.quantize(v, vs)
+    out = O.attend_int8(qb, kq, ks, vq, vs, torch.ones(2, 3, 1, dtype=torch.bool), 0.1, O.CFG32)
+    G = qb.shape[2] // k.shape[2]
+    expect = (vq.double() * vs.double())[:, 0].repeat_interleave(G, dim=1)      # [b, Hq, D]
+    assert torch.allclose(out.double(), expect[:, None].expand_as(out), rtol=1e-6, atol=1e-7)
+
+
+def test_identical_keys_give_mean_of_v():
+    qb, k, v = _dense_case(K=45)
+    k[:] = k[:, :1]
+    ks = O.scale_from_absmax(k.abs().amax(dim=(0, 1), keepdim=True))
+    vs = O.scale_from_absmax(v.abs().amax(dim=(0, 1), keepdim=True))
+    kq, vq = O.quantize(k, ks), O.quantize(v, vs)
+    out = O.attend_int8(qb, kq, ks, vq, vs, torch.ones(2, 3, 45, dtype=torch.bool), 0.1, O.CFG32)
+    G = qb.shape[2] // k.shape[2]
+    expect = (vq.double() * vs.double()).mean(1).repeat_interleave(G, dim=1)
+    assert torch.allclose(out.double(), expect[:, None].expand_as(out), rtol=1e-6, atol=1e-7)
+
+
+def _brute_force_b(q, kq, vq, ks, vs, scale, lim, p_tile=32):
+    """Implementation B for one request, written as explicit per-row loops in numpy.
+    q [n, Hq, D] float, kq/vq [L, Hkv, D] int8, ks/vs [Hkv, D|1], lim[t] = visible keys of token t."""
+    n, hq, D = q.shape
+    L, hkv, _ = kq.shape
+    G = hq // hkv
+    out = np.zeros((n, hq, D), dtype=np.float32)
+    K, V = kq.numpy().astype(np.float64), vq.numpy().astype(np.float64)
+    ksd, vsd = ks.numpy().astype(np.float64), vs.numpy().astype(np.float64)
+    for t in range(n):
+        for h in range(hq):
+            j = h // G
+            x = q[t, h].numpy().astype(np.float64)
+            if ksd.shape[1] > 1:
+                x = x * ksd[j]
+                post = 1.0
+            else:
+                post = ksd[j, 0]
+            sq = max(np.abs(x).max() / 127.0, 1e-8)
+            codes = np.clip(np.round(x.astype(np.float32).astype(np.float64) / sq), -127, 127)
+            s = np.array([(codes * K[i, j]).sum() * sq * post * scale for i in range(L)]).astype(np.float32)
+            vis = np.arange(L) < lim[t]
+            s = np.where(vis, s, np.float32(-np.inf)).astype(np.float32)
+            e = np.exp((s - s.max()).astype(np.float32)).astype(np.float32)
+            eh = np.zeros_like(e)
+            for a in range(0, L, p_tile):
+                tile = e[a:a + p_tile]
+                st = np.float32(max(np.float32(tile.max() / np.float32(127.0)), np.float32(1e-30)))
+                eh[a:a + p_tile] = (np.round(tile / st).astype(np.float32) * st).astype(np.float32)
+            den = eh.sum(dtype=np.float32)
+            o = (eh.astype(np.float64)[:, None] * V[:, j]).sum(0) / float(den)
+            out[t, h] = (o * vsd[j]).astype(np.float32)
+    return torch.from_numpy(out)
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+@pytest.mark.parametrize("n,L", [(1, 70), (3, 40), (5, 5)])
+def test_attend_int8_matches_brute_force(per_channel, n, L):
+    gen = torch.Generator().manual_seed(n * 100 + L)
+    hq, hkv, D = 6, 2, 16
+    q = torch.randn(n, hq, D, generator=gen) * 2
+    k = torch.randn(L, hkv, D, generator=gen) * 3
+    v = torch.randn(L, hkv, D, generator=gen)
+    if per_channel:
+        ks = O.scale_from_absmax(k.abs().amax(0))
+        vs = O.scale_from_absmax(v.abs().amax(0))
+    else:
+        ks = O.scale_from_absmax(k.abs().amax(0).amax(-1, keepdim=True))
+        vs = O.scale_from_absmax(v.abs().amax(0).amax(-1, keepdim=True))
+    kq, vq = O.quantize(k, ks), O.quantize(v, vs)
+    lim = [L - n + 1 + t for t in range(n)]
+    mask = torch.tensor([[i < lim[t] for i in range(L)] for t in range(n)])
+    out = O.attend_int8(q[None], kq[None], ks[None, None], vq[None], vs[None, None], mask[None], 0.3, O.CFG32)[0]
+    bf = _brute_force_b(q, kq, vq, ks, vs, 0.3, lim)
+    assert torch.allclose(out, bf, rtol=1e-5, atol=1e-6)
+    if L > 32:   # the checker is sensitive: a 64-key P tile (a plausible mistake) is caught
+        wrong = _brute_force_b(q, kq, vq, ks, vs, 0.3, lim, p_tile=64)
+        assert not torch.allclose(out, wrong, rtol=1e-5, atol=1e-6)
+
+
+def test_run_paged_matches_dense_loop():
+    """run_paged's gathering, padding and bottom-right causal mask vs a per-request dense loop."""
+    c = synth_case = cases.synth.paged_case(4, 2, [1, 3, 1, 2], [5, 20, 33, 2], head_dim=16, seed=3, dist="randn")
+    out = O.paged_attention_ref(c["q"], c["k"], c["v"], c["cu"], c["seq_lens"], c["block_table"], 0.25)
+    bs = c["k"].shape[1]
+    cu = c["cu"].tolist()
+    for r, L in enumerate(synth_case["seq_lens"].tolist()):
+        pages = c["block_table"][r, :-(-L // bs)].long()
+        k = c["k"][pages].reshape(-1, 2, 16)[:L].float()
+        v = c["v"][pages].reshape(-1, 2, 16)[:L].float()
+        n = cu[r + 1] - cu[r]
+        for t in range(n):
+            vis = L - n + 1 + t
+            for h in range(4):
+                s = (k[:vis, h // 2] @ c["q"][cu[r] + t, h].float()) * 0.25
+                o = torch.softmax(s, 0) @ v[:vis, h // 2]
+                assert torch.allclose(out[cu[r] + t, h].float(), o, atol=1e-2, rtol=1e-2)
+
+
+# ---------------------------------------------------------------- plan_long (host)
+@pytest.mark.parametrize("plan_fn", ["oracle", "product"])
+def test_plan_long_page_table_kat(plan_fn):
+    """Known-answer test of tests/test_cuda_kernels.py:88-97."""
+    cu = torch.tensor([0, 1, 13, 14, 314], dtype=torch.int32)        # q_lens 1, 12, 1, 300
+    sl = torch.tensor([50, 40, 9, 330], dtype=torch.int32)
+    if plan_fn == "oracle":
+        p = O.plan_long_ref(cu, sl, 16)
+        src_req, src_j, bt, mk, hs = p["src_req"], p["src_j"], p["block_table"], p["max_seqlen_k"], p["has_short"]
+        none = O.plan_long_ref(torch.tensor([0, 1, 9]), torch.tensor([5, 8]), 16)
+    else:
+        p = ck.plan_long(cu, sl, 16)
+        src_req, src_j, bt, mk, hs = p.src_req, p.src_j, p.block_table, p.max_seqlen_k, p.has_short
+        none = ck.plan_long(torch.tensor([0, 1, 9]), torch.tensor([5, 8]), 16)
+    assert mk == 330 and hs
+    assert src_req.tolist() == [1] * 3 + [3] * 21 and src_j.tolist() == list(range(3)) + list(range(21))
+    assert bt[1, :3].tolist() == [0, 1, 2] and bt[3, :21].tolist() == list(range(3, 24))
+    assert bt.shape[1] * 16 >= 330 + 256 and not bt[3, 21:].any()
+    assert none is None
+
+
+def test_plan_long_product_matches_oracle_random():
+    r = np.random.Generator(np.random.PCG64(8))
+    for _ in range(50):
+        n = int(r.integers(1, 20))
+        ql = r.integers(0, 40, n)
+        sl = ql + r.integers(0, 500, n)
+        cu = np.concatenate([[0], np.cumsum(ql)])
+        a, b = O.plan_long_ref(cu, sl, 16), ck.plan_long(cu, sl, 16)
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert np.array_equal(a["src_req"], b.src_req) and np.array_equal(a["src_j"], b.src_j)
+            assert np.array_equal(a["block_table"], b.block_table)
+            assert a["max_seqlen_k"] == b.max_seqlen_k and a["has_short"] == b.has_short
