@@ -115,7 +115,7 @@ def time_c2(w, steps, warmup):
 
 
 # ------------------------------------------------------------------------------------------------ CPU baseline
-def cpu_baseline(w, out, budget_s=12.0, max_reqs=32):
+def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
     """The CPU oracle (port of int8_ref B + run_paged) on whole c2 requests until ~budget_s of CPU work;
     also the parity of the GPU output on those requests."""
     sys.path.insert(0, REPO)
@@ -266,12 +266,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy 5 times (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (every kernel shards per request / "
               "kv head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=DEV)
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 1 << 30, "copies": 5}))
+        return
     ck.ext()
     print("# building c2 workload", file=sys.stderr, flush=True)
     w = build_c2()
@@ -298,6 +309,13 @@ def main():
                      "kernel": "attn_kernel<128,1>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
+    prof = os.path.join(REPO, "profiles", "attn_kernel_c2_traffic.json")
+    if os.path.exists(prof):   # HBM bytes per launch from the committed rocprofv3 --pmc runs of this workload
+        with open(prof) as f:
+            t = json.load(f)
+        res["roofline"]["traffic"] = t["traffic_bytes"]
+        res["roofline"]["traffic_source"] = "profiles/attn_kernel_c2_decode_128x32k.md (FETCH_SIZE x %.3f + WRITE_SIZE x %.3f)" % (
+            t["fetch_factor"], t["write_factor"])
     if not args.no_cpu:
         print("# cpu baseline", file=sys.stderr, flush=True)
         res["cpu_baseline"], res["parity"] = cpu_baseline(w, out)
