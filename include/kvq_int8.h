@@ -63,10 +63,13 @@ int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, i
  * Replaces the pybind op int8_decode_attention (reference kvq/cuda/int8_kv.cu:600-648, kernels
  * :168-463 and :472-503), bound as kvq/cuda_kernels.py:51-58 decode_attention.
  * Requests with q_len == 0 or q_len > qmax are skipped (their out rows untouched).
- * num_splits == 1: out written directly, segm_* ignored (may be NULL).
- * num_splits  > 1 (<= 64): the context is split in num_splits ranges of whole 32-key tiles; partials
- *   go to segm_out [T, Hq, S, D], segm_max / segm_sum [T, Hq, S] (fp32; element (t, h, s) at
- *   t * seg_st + h * seg_sh + s, segm_out at that index * D + d) and a second kernel merges them. */
+ * num_splits == 1: every context in one pass, out written directly, segm_* ignored (may be NULL).
+ * num_splits  > 1 (<= 64): the most splits a request may use. Each request's context is cut into
+ *   ranges of whole 32-key tiles, as few as spread the batch's tiles over about target_waves
+ *   wavefronts (0 = 8 per compute unit), at most num_splits, none under 128 keys. A request left with
+ *   one range writes out directly; the others write partials to segm_out [T, Hq, S, D] and
+ *   segm_max / segm_sum [T, Hq, S] (fp32; element (t, h, s) at t * seg_st + h * seg_sh + s, segm_out
+ *   at that index * D + d), which a second kernel merges. */
 int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
                               int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
                               int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
@@ -76,7 +79,7 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               const float* k_scale, int64_t k_scale_cols, const float* v_scale,
                               int64_t v_scale_cols, double softmax_scale, float* segm_out, float* segm_max,
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
-                              int64_t max_query_len, int64_t qmax, void* stream);
+                              int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
 
 /* Dequantize pages of the INT8 cache into a contiguous bf16 cache [P, bs, H, D] (long-query path).
  * Replaces the pybind op dequant_pages (reference kvq/cuda/int8_kv.cu:650-672, kernel :505-542),

@@ -27,6 +27,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/kvq_int8.h"
@@ -40,7 +41,10 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int WAVE = 64;
 constexpr int TILE = 32;          // keys per attention tile = P quantization tile
 constexpr int MAX_SPLITS = 64;    // split_reduce_kernel keeps one split per lane
-constexpr int MAX_ROW_TILES = 4;  // 16-row tiles per wavefront (64 (token, q head) rows)
+constexpr int MAX_ROW_TILES = 4;  // row tiles (wavefronts) per attention workgroup
+constexpr int MIN_SPLIT_TILES = 4;  // shortest split: 4 tiles = 128 keys
+constexpr int DEFAULT_WAVES_PER_CU = 8;
+constexpr int DEFAULT_PREFETCH = 3;
 
 // ------------------------------------------------------------------------------------------------
 // Scalar helpers
@@ -92,13 +96,42 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // ------------------------------------------------------------------------------------------------
 // Fused quantize + reshape_and_cache (reference kvq/cuda/int8_kv.cu:55-84).
-// Each lane owns 16 channels of one head for the whole launch (scales and their reciprocals stay in
-// registers) and walks the tokens with a grid stride. Per (token, head) the K and V rows are read
-// as 32-byte runs and the codes written as one 16-byte store each, so the 256-byte K|V run of a
-// slot in vLLM's interleaved layout is written by 16 consecutive lanes.
+// A wavefront covers whole tokens: each lane owns 8 channels of one head for the whole launch (their
+// reciprocal scales and K means stay in registers), so a token's K and V rows are read as 1 KB
+// contiguous runs (H = 4, D = 128) and each (token, head) writes its 128-byte K and V code rows with
+// 16 consecutive lanes -- the 256-byte K|V run of a slot in vLLM's interleaved layout. Every lane
+// issues the loads of QC_UNROLL tokens before converting any of them.
 // ------------------------------------------------------------------------------------------------
-constexpr int QC_CPL = 16;   // channels per lane
+constexpr int QC_CPL = 8;     // channels per lane
+constexpr int QC_UNROLL = 4;  // tokens per lane and step
 constexpr int QC_BLOCK = 256;
+
+// Codes of 8 channels (one 16-byte bf16 run) packed little endian into 2 dwords; K subtracts mu.
+// Fast path with v_rcp reciprocals; a lane whose quotient lies near a rounding boundary redoes its
+// 8 channels with IEEE division (scales re-read from memory).
+template <bool SUB_MU>
+__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const float (&mu)[QC_CPL],
+                                        const float* __restrict__ s, int s_pc) {
+  float x[QC_CPL], c[QC_CPL];
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bf16_lo(wd[j]);
+    x[2 * j + 1] = bf16_hi(wd[j]);
+  }
+  if (SUB_MU) {
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) x[e] = x[e] - mu[e];
+  }
+  bool bad = false;
+#pragma unroll
+  for (int e = 0; e < QC_CPL; ++e) c[e] = code_fast(x[e], r[e], bad);
+  if (bad) {
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) c[e] = code_exact(x[e], s[s_pc ? e : 0]);
+  }
+  return u32x2{pack_i8x4(c[0], c[1], c[2], c[3]), pack_i8x4(c[4], c[5], c[6], c[7])};
+}
 
 template <int D>
 __global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
@@ -113,59 +146,39 @@ __global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
   if ((int)threadIdx.x >= tpb * ipt) return;
   const int item = threadIdx.x % ipt;
   const int h = item / LPH, d0 = (item % LPH) * QC_CPL;
-
-  float kr[QC_CPL], vr[QC_CPL], kS[QC_CPL], vS[QC_CPL], mu[QC_CPL];
+  const float* ksp = ks + (ks_pc ? h * D + d0 : h);
+  const float* vsp = vs + (vs_pc ? h * D + d0 : h);
+  float kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
 #pragma unroll
   for (int e = 0; e < QC_CPL; ++e) {
-    const int c = h * D + d0 + e;
-    kS[e] = ks[ks_pc ? c : h];
-    vS[e] = vs[vs_pc ? c : h];
-    kr[e] = __builtin_amdgcn_rcpf(kS[e]);
-    vr[e] = __builtin_amdgcn_rcpf(vS[e]);
-    mu[e] = kmu[c];
+    kr[e] = __builtin_amdgcn_rcpf(ksp[ks_pc ? e : 0]);
+    vr[e] = __builtin_amdgcn_rcpf(vsp[vs_pc ? e : 0]);
+    mu[e] = kmu[h * D + d0 + e];
   }
   const int64_t bmask = (int64_t(1) << lbs) - 1;
-  for (int t = blockIdx.x * tpb + threadIdx.x / ipt; t < n; t += gridDim.x * tpb) {
-    const int64_t slot = slots[t];
-    if (slot < 0 || slot >= num_slots) continue;
-    const u32x4* kp = reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0);
-    const u32x4* vp = reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0);
-    const u32x4 ka = kp[0], kb = kp[1], va = vp[0], vb = vp[1];
-    const uint32_t kw[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
-    const uint32_t vw[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
-    float kx[QC_CPL], vx[QC_CPL], kq[QC_CPL], vq[QC_CPL];
-    bool bad = false;
+  const int stride = gridDim.x * tpb;
+  for (int t0 = blockIdx.x * tpb + threadIdx.x / ipt; t0 < n; t0 += QC_UNROLL * stride) {
+    int64_t slot[QC_UNROLL];
+    u32x4 kin[QC_UNROLL], vin[QC_UNROLL];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      kx[2 * j] = bf16_lo(kw[j]) - mu[2 * j];
-      kx[2 * j + 1] = bf16_hi(kw[j]) - mu[2 * j + 1];
-      vx[2 * j] = bf16_lo(vw[j]);
-      vx[2 * j + 1] = bf16_hi(vw[j]);
-    }
-#pragma unroll
-    for (int e = 0; e < QC_CPL; ++e) {
-      kq[e] = code_fast(kx[e], kr[e], bad);
-      vq[e] = code_fast(vx[e], vr[e], bad);
-    }
-    if (bad) {  // a quotient within a few ulp of a rounding boundary: redo this lane exactly
-#pragma unroll
-      for (int e = 0; e < QC_CPL; ++e) {
-        kq[e] = code_exact(kx[e], kS[e]);
-        vq[e] = code_exact(vx[e], vS[e]);
+    for (int u = 0; u < QC_UNROLL; ++u) {
+      const int t = t0 + u * stride;
+      slot[u] = -1;
+      if (t < n) {
+        slot[u] = slots[t];
+        kin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0));
+        vin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0));
       }
     }
-    const int64_t blk = slot >> lbs, off = slot & bmask;
-    u32x4 ko, vo;
-    ko.x = pack_i8x4(kq[0], kq[1], kq[2], kq[3]);
-    ko.y = pack_i8x4(kq[4], kq[5], kq[6], kq[7]);
-    ko.z = pack_i8x4(kq[8], kq[9], kq[10], kq[11]);
-    ko.w = pack_i8x4(kq[12], kq[13], kq[14], kq[15]);
-    vo.x = pack_i8x4(vq[0], vq[1], vq[2], vq[3]);
-    vo.y = pack_i8x4(vq[4], vq[5], vq[6], vq[7]);
-    vo.z = pack_i8x4(vq[8], vq[9], vq[10], vq[11]);
-    vo.w = pack_i8x4(vq[12], vq[13], vq[14], vq[15]);
-    *reinterpret_cast<u32x4*>(kc + blk * kc_sb + off * kc_sn + h * kc_sh + d0) = ko;
-    *reinterpret_cast<u32x4*>(vc + blk * vc_sb + off * vc_sn + h * vc_sh + d0) = vo;
+#pragma unroll
+    for (int u = 0; u < QC_UNROLL; ++u) {
+      if (slot[u] < 0 || slot[u] >= num_slots) continue;   // padding (or out of range): skipped
+      const int64_t blk = slot[u] >> lbs, off = slot[u] & bmask;
+      __builtin_nontemporal_store(quant8<true>(kin[u], kr, mu, ksp, ks_pc),
+                                  reinterpret_cast<u32x2*>(kc + blk * kc_sb + off * kc_sn + h * kc_sh + d0));
+      __builtin_nontemporal_store(quant8<false>(vin[u], vr, mu, vsp, vs_pc),
+                                  reinterpret_cast<u32x2*>(vc + blk * vc_sb + off * vc_sn + h * vc_sh + d0));
+    }
   }
 }
 
@@ -216,13 +229,44 @@ struct AttnArgs {
   const float* ks;
   const float* vs;
   int64_t q_st, q_sh, o_st, o_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, seg_st, seg_sh, bt_stride;
-  float sm_log2;  // softmax_scale * log2(e)
-  int num_blocks, lbs, G, num_splits, qmax, row_groups, ks_pc, vs_pc;
+  float sm_log2;      // softmax_scale * log2(e)
+  int num_blocks, lbs, G, qmax, ks_pc, vs_pc;
+  int num_seqs, hkv;
+  int max_splits;     // splits per request in the grid (an upper bound: requests use what they need)
+  int row_tiles;      // 16-row tiles of (token, q head) rows per (request, kv head)
+  int waves;          // wavefronts per workgroup: consecutive row tiles of one (request, kv head, split)
+  int min_tiles;      // shortest split, in 32-key tiles
+  int64_t target_waves;  // the batch's tiles are spread over about this many wavefronts
 };
+
+// 32-key tiles per split of a request with `ntiles` tiles: at most max_splits splits, and long enough
+// that the whole batch (its tiles x kv heads x row tiles) spreads over about target_waves wavefronts,
+// never shorter than min_tiles. The attention kernel and the merge both evaluate it (one whole
+// wavefront, identical integer arithmetic), so they agree on every request's split count.
+__device__ int split_len(const AttnArgs& a, int ntiles, int lane) {
+  if (a.max_splits == 1) return ntiles > 0 ? ntiles : 1;
+  long long part = 0;
+  for (int r = lane; r < a.num_seqs; r += WAVE) part += (a.seq_lens[r] + TILE - 1) / TILE;
+#pragma unroll
+  for (int o = 32; o; o >>= 1) part += __shfl_xor(part, o, WAVE);
+  const long long units = part * a.hkv * a.row_tiles;
+  const long long target = (units + a.target_waves - 1) / a.target_waves;
+  const int per = (ntiles + a.max_splits - 1) / a.max_splits;
+  // the reduction leaves every lane with the same value; say so, so that the loop bounds (and the
+  // block-table reads they guard) stay scalar
+  return __builtin_amdgcn_readfirstlane(
+      (int)std::max<long long>(std::max<long long>(per, target), std::max(a.min_tiles, 1)));
+}
+
+// K/V pages are streamed exactly once per launch: the non-temporal hint keeps them from evicting
+// what is reused (block tables, q, scales) from L2 and the last-level cache (measured on c2:
+// 771 -> 688 us).
+__device__ __forceinline__ i32x4 ldk(const i32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ u32x2 ldv(const u32x2* p) { return __builtin_nontemporal_load(p); }
 
 template <int D>
 struct KVTile {
-  i32x4 k[2][D / 64];   // QK A operands: keys 16b + m, bytes = channels (D/4) g + 16 s + j
+  i32x4 k[2][D / 64];     // QK A operands: keys 16b + m, bytes = channels (D/4) g + 16 s + j
   uint32_t v[8][D / 64];  // V rows: keys 16 (j / 4) + 4 g + j % 4, channels (D/16) m + 0..D/16-1
 };
 
@@ -239,34 +283,39 @@ __device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t 
   o3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
-template <int D, int NRT>
-__global__ __launch_bounds__(WAVE) void attn_kernel(AttnArgs a) {
+// One wavefront = one 16-row tile of one (request, kv head, split); a workgroup holds `waves`
+// consecutive row tiles of the same (request, kv head, split), which stream the same K/V tiles at
+// the same time (the second and later reads hit L1/L2).
+template <int D, int PF>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   constexpr int KPL = D / 4;        // K bytes per lane and key
   constexpr int KSTEPS = D / 64;    // x64 MFMAs per 16-key block
   constexpr int VT = D / 16;        // PV channel tiles = V bytes per lane and key
   constexpr int VW = D / 64;        // V dwords per lane and key
-  const int lane = threadIdx.x, n = lane & 15, g = lane >> 4;
+  // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
+  const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int n = lane & 15, g = lane >> 4;
   const int seq = blockIdx.x, kvh = blockIdx.y;
-  const int split = blockIdx.z % a.num_splits, rg = blockIdx.z / a.num_splits;
+  const int split = blockIdx.z % a.max_splits, rg = blockIdx.z / a.max_splits;
   const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
   const int G = a.G;
-  const int row0 = rg * 16 * NRT;  // first (token, q head) row of this wavefront
+  const int row0 = (rg * a.waves + wave) * 16;  // first (token, q head) row of this wavefront
   if (qlen == 0 || qlen > a.qmax || row0 >= qlen * G) return;
   const int L = a.seq_lens[seq];
   const int ntiles = (L + TILE - 1) / TILE;
-  const int per = (ntiles + a.num_splits - 1) / a.num_splits;
+  const int per = split_len(a, ntiles, lane);
+  const int nsplit = ntiles > 0 ? (ntiles + per - 1) / per : 1;
+  if (split >= nsplit) return;
   const int c_begin = split * per, c_end = min(ntiles, c_begin + per);
   const int* bt = a.block_table + (int64_t)seq * a.bt_stride;
   const int bs = 1 << a.lbs;
 
   // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
-  i32x4 qop[NRT][KSTEPS];
-  float rs[NRT];
-  int lim[NRT];
-  const float kvh_ks = a.ks_pc ? 1.f : a.ks[kvh];
-#pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    const int R = row0 + 16 * rt + n, rtok = R / G, rh = R % G;
+  i32x4 qop[KSTEPS];
+  const int R = row0 + n, rtok = R / G, rh = R % G;
+  float rs;
+  int lim;
+  {
     float x[KPL];
     float amax = 0.f;
     if (rtok < qlen) {
@@ -302,22 +351,17 @@ __global__ __launch_bounds__(WAVE) void attn_kernel(AttnArgs a) {
         w[u] = (int)pack_i8x4(code_exact(x[e], s), code_exact(x[e + 1], s), code_exact(x[e + 2], s),
                               code_exact(x[e + 3], s));
       }
-      qop[rt][st] = w;
+      qop[st] = w;
     }
-    rs[rt] = s * kvh_ks * a.sm_log2;
-    lim[rt] = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
+    rs = s * (a.ks_pc ? 1.f : a.ks[kvh]) * a.sm_log2;
+    lim = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
   }
   // every row of this wavefront sees at least keys < lim_lo
   const int lim_lo = L - qlen + 1 + row0 / G;
 
-  float m[NRT], l[NRT], acc[NRT][VT][4];
+  float m = -1e30f, l = 0.f, acc[VT][4];
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    m[rt] = -1e30f;
-    l[rt] = 0.f;
-#pragma unroll
-    for (int t = 0; t < VT; ++t) acc[rt][t][0] = acc[rt][t][1] = acc[rt][t][2] = acc[rt][t][3] = 0.f;
-  }
+  for (int t = 0; t < VT; ++t) acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.f;
 
   const int8_t* kbase = a.kc + (int64_t)kvh * a.k_sh;
   const int8_t* vbase = a.vc + (int64_t)kvh * a.v_sh;
@@ -340,36 +384,34 @@ __global__ __launch_bounds__(WAVE) void attn_kernel(AttnArgs a) {
     const int8_t* vb1 = vbase + (int64_t)p1 * a.v_sb + (int64_t)o1 * a.v_sn;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
-      r.k[0][s] = *reinterpret_cast<const i32x4*>(kb0 + koff + 16 * s);
-      r.k[1][s] = *reinterpret_cast<const i32x4*>(kb1 + koff + 16 * s);
+      r.k[0][s] = ldk(reinterpret_cast<const i32x4*>(kb0 + koff + 16 * s));
+      r.k[1][s] = ldk(reinterpret_cast<const i32x4*>(kb1 + koff + 16 * s));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (VW == 2) {
-        const u32x2 w0 = *reinterpret_cast<const u32x2*>(vb0 + voff + i * vsn);
-        const u32x2 w1 = *reinterpret_cast<const u32x2*>(vb1 + voff + i * vsn);
+        const u32x2 w0 = ldv(reinterpret_cast<const u32x2*>(vb0 + voff + i * vsn));
+        const u32x2 w1 = ldv(reinterpret_cast<const u32x2*>(vb1 + voff + i * vsn));
         r.v[i][0] = w0.x; r.v[i][1] = w0.y;
         r.v[4 + i][0] = w1.x; r.v[4 + i][1] = w1.y;
       } else {
-        r.v[i][0] = *reinterpret_cast<const uint32_t*>(vb0 + voff + i * vsn);
-        r.v[4 + i][0] = *reinterpret_cast<const uint32_t*>(vb1 + voff + i * vsn);
+        r.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb0 + voff + i * vsn));
+        r.v[4 + i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb1 + voff + i * vsn));
       }
     }
   };
 
   auto compute = [&](const KVTile<D>& r, int c) {
     const int n0 = c * TILE;
-    // ---- QK ----
-    i32x4 sc[NRT][2];
+    // ---- QK: S^T[key][row] for the tile's two 16-key blocks ----
+    i32x4 sc[2];
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt)
+    for (int b = 0; b < 2; ++b) {
+      i32x4 z = {0, 0, 0, 0};
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        i32x4 z = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) z = __builtin_amdgcn_mfma_i32_16x16x64_i8(r.k[b][s], qop[rt][s], z, 0, 0, 0);
-        sc[rt][b] = z;
-      }
+      for (int s = 0; s < KSTEPS; ++s) z = __builtin_amdgcn_mfma_i32_16x16x64_i8(r.k[b][s], qop[s], z, 0, 0, 0);
+      sc[b] = z;
+    }
     // ---- V^T operands: 8x8 byte transpose per channel tile ----
     long vop[VT];
     if constexpr (VW == 2) {
@@ -389,150 +431,135 @@ __global__ __launch_bounds__(WAVE) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int t = 0; t < VT; ++t) vop[t] = (long)(((uint64_t)hi[t] << 32) | lo[t]);
     }
+    // ---- online softmax; key of accumulator (b, i) = n0 + 16 b + 4 g + i ----
     const bool full = n0 + TILE <= lim_lo;  // no key of this tile is masked for any row
-    bool rescale = false;
-    float alpha[NRT], ps[NRT];
-    long pop[NRT];
+    int mx = INT32_MIN;
+    bool ok[2][4];
 #pragma unroll
-    for (int rt = 0; rt < NRT; ++rt) {
-      // key of accumulator (b, i) = n0 + 16 b + 4 g + i
-      int mx = INT32_MIN;
-      bool ok[2][4];
+    for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ok[b][i] = full || n0 + 16 * b + 4 * g + i < lim[rt];
-          mx = ok[b][i] ? max(mx, sc[rt][b][i]) : mx;
-        }
-      mx = max(mx, __shfl_xor(mx, 16, WAVE));
-      mx = max(mx, __shfl_xor(mx, 32, WAVE));
-      const float tmax = mx == INT32_MIN ? -INFINITY : (float)mx * rs[rt];
-      const float mnew = __builtin_fmaxf(m[rt], tmax);
-      alpha[rt] = __builtin_amdgcn_exp2f(m[rt] - mnew);
-      m[rt] = mnew;
-      rescale |= alpha[rt] != 1.f;
-      const float pm = __builtin_amdgcn_exp2f(tmax - mnew);  // max of this tile's P (exp2 is monotone)
-      ps[rt] = __builtin_fmaxf(pm / 127.f, 1e-30f);
-      const float ri = __builtin_amdgcn_rcpf(ps[rt]);
-      float pc[2][4];
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[rt][b][i], rs[rt], -mnew));
-          pc[b][i] = ok[b][i] ? __builtin_fminf(__builtin_rintf(p * ri), 127.f) : 0.f;
-        }
-      const uint32_t p0 = pack_i8x4(pc[0][0], pc[0][1], pc[0][2], pc[0][3]);
-      const uint32_t p1 = pack_i8x4(pc[1][0], pc[1][1], pc[1][2], pc[1][3]);
-      pop[rt] = (long)(((uint64_t)p1 << 32) | p0);
-      const float psum = (pc[0][0] + pc[0][1]) + (pc[0][2] + pc[0][3]) + (pc[1][0] + pc[1][1]) + (pc[1][2] + pc[1][3]);
-      l[rt] = __builtin_fmaf(psum, ps[rt], l[rt] * alpha[rt]);
-    }
-    if (__any(rescale)) {
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt)
-#pragma unroll
-        for (int t = 0; t < VT; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[rt][t][i] *= alpha[rt];
-    }
-    // ---- PV ----
-#pragma unroll
-    for (int t = 0; t < VT; ++t)
-#pragma unroll
-      for (int rt = 0; rt < NRT; ++rt) {
-        i32x4 z = {0, 0, 0, 0};
-        z = __builtin_amdgcn_mfma_i32_16x16x32_i8(vop[t], pop[rt], z, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[rt][t][i] = __builtin_fmaf((float)z[i], ps[rt], acc[rt][t][i]);
+      for (int i = 0; i < 4; ++i) {
+        ok[b][i] = full || n0 + 16 * b + 4 * g + i < lim;
+        mx = ok[b][i] ? max(mx, sc[b][i]) : mx;
       }
+    mx = max(mx, __shfl_xor(mx, 16, WAVE));
+    mx = max(mx, __shfl_xor(mx, 32, WAVE));
+    const float tmax = mx == INT32_MIN ? -INFINITY : (float)mx * rs;
+    const float mnew = __builtin_fmaxf(m, tmax);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    const float pm = __builtin_amdgcn_exp2f(tmax - mnew);  // max of this tile's P (exp2 is monotone)
+    const float ps = __builtin_fmaxf(pm / 127.f, 1e-30f);
+    const float ri = __builtin_amdgcn_rcpf(ps);
+    float pc[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[b][i], rs, -mnew));
+        pc[b][i] = ok[b][i] ? __builtin_fminf(__builtin_rintf(p * ri), 127.f) : 0.f;
+      }
+    const uint32_t p0 = pack_i8x4(pc[0][0], pc[0][1], pc[0][2], pc[0][3]);
+    const uint32_t p1 = pack_i8x4(pc[1][0], pc[1][1], pc[1][2], pc[1][3]);
+    const long pop = (long)(((uint64_t)p1 << 32) | p0);
+    const float psum = (pc[0][0] + pc[0][1]) + (pc[0][2] + pc[0][3]) + (pc[1][0] + pc[1][1]) + (pc[1][2] + pc[1][3]);
+    l = __builtin_fmaf(psum, ps, l * alpha);
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] *= alpha;
+    }
+    // ---- PV: O^T[channel][row] += (V^T . P^T) * ps ----
+#pragma unroll
+    for (int t = 0; t < VT; ++t) {
+      i32x4 z = {0, 0, 0, 0};
+      z = __builtin_amdgcn_mfma_i32_16x16x32_i8(vop[t], pop, z, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf((float)z[i], ps, acc[t][i]);
+    }
   };
 
-  // ---- main loop, one tile of prefetch ----
+  // ---- main loop: a ring of PF register tiles, PF - 1 of them in flight while one is computed.
+  // Loads are never skipped (past the end they re-read the last tile, an L2 hit), so every wait
+  // in the loop is for exactly the oldest tile. ----
   if (c_begin < c_end) {
-    KVTile<D> A, B;
-    int c = c_begin;
-    load(A, c);
-    while (true) {
-      if (c + 1 < c_end) load(B, c + 1);
-      compute(A, c);
-      if (++c >= c_end) break;
-      if (c + 1 < c_end) load(A, c + 1);
-      compute(B, c);
-      if (++c >= c_end) break;
+    KVTile<D> ring[PF];
+    const int c_last = c_end - 1;
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) load(ring[j], min(c_begin + j, c_last));
+    for (int c0 = c_begin; c0 < c_end; c0 += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int c = c0 + j;
+        if (c >= c_end) break;
+        load(ring[(j + PF - 1) % PF], min(c + PF - 1, c_last));
+        compute(ring[j], c);
+      }
     }
   }
 
-  // ---- epilogue ----
+  // ---- epilogue: lane (n, g) holds channels (D/4) g + (D/16) i + t of row n ----
+  l += __shfl_xor(l, 16, WAVE);
+  l += __shfl_xor(l, 32, WAVE);
+  if (rtok >= qlen) return;
+  constexpr int OPL = D / 4;
+  const int head = kvh * G + rh;
+  const int qt = tok + rtok;
+  float vsc[OPL];
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    l[rt] += __shfl_xor(l[rt], 16, WAVE);
-    l[rt] += __shfl_xor(l[rt], 32, WAVE);
-  }
-  constexpr int OPL = D / 4;  // output channels per lane: OPL * g + 8 i + t  (D = 128), 4 i + t (D = 64)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-  for (int rt = 0; rt < NRT; ++rt) {
-    const int R = row0 + 16 * rt + n, rtok = R / G;
-    if (rtok >= qlen) continue;
-    const int head = kvh * G + R % G;
-    const int qt = tok + rtok;
-    float vsc[OPL];
+    for (int t = 0; t < VT; ++t) vsc[VT * i + t] = a.vs_pc ? a.vs[kvh * D + OPL * g + VT * i + t] : a.vs[kvh];
+  if (nsplit == 1) {
+    const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
+    uint32_t o[OPL / 2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int t = 0; t < VT; ++t) vsc[VT * i + t] = a.vs_pc ? a.vs[kvh * D + OPL * g + VT * i + t] : a.vs[kvh];
-    if (a.num_splits == 1) {
-      const float inv = 1.f / __builtin_fmaxf(l[rt], 1e-30f);
-      uint32_t o[OPL / 2];
+      for (int t = 0; t < VT; t += 2)
+        o[(VT * i + t) / 2] = pack_bf16x2((acc[t][i] * inv) * vsc[VT * i + t], (acc[t + 1][i] * inv) * vsc[VT * i + t + 1]);
+    u32x4* op = reinterpret_cast<u32x4*>(a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + OPL * g);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int u = 0; u < OPL / 8; ++u) op[u] = u32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
+  } else {
+    const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + split;
+    if (g == 0) {
+      a.segm_max[sidx] = m;
+      a.segm_sum[sidx] = l;
+    }
+    float* sp = a.segm_out + sidx * D + OPL * g;
 #pragma unroll
-        for (int t = 0; t < VT; t += 2)
-          o[(VT * i + t) / 2] = pack_bf16x2((acc[rt][t][i] * inv) * vsc[VT * i + t],
-                                            (acc[rt][t + 1][i] * inv) * vsc[VT * i + t + 1]);
-      u32x4* op = reinterpret_cast<u32x4*>(a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + OPL * g);
-#pragma unroll
-      for (int u = 0; u < OPL / 8; ++u) op[u] = u32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
-    } else {
-      const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + split;
-      if (g == 0) {
-        a.segm_max[sidx] = m[rt];
-        a.segm_sum[sidx] = l[rt];
-      }
-      float* sp = a.segm_out + sidx * D + OPL * g;
-#pragma unroll
-      for (int u = 0; u < OPL / 4; ++u) {
-        float4 w;
-        const int c0 = 4 * u;
-        w.x = acc[rt][(c0 + 0) % VT][(c0 + 0) / VT] * vsc[c0 + 0];
-        w.y = acc[rt][(c0 + 1) % VT][(c0 + 1) / VT] * vsc[c0 + 1];
-        w.z = acc[rt][(c0 + 2) % VT][(c0 + 2) / VT] * vsc[c0 + 2];
-        w.w = acc[rt][(c0 + 3) % VT][(c0 + 3) / VT] * vsc[c0 + 3];
-        reinterpret_cast<float4*>(sp)[u] = w;
-      }
+    for (int u = 0; u < OPL / 4; ++u) {
+      float4 w;
+      const int c0 = 4 * u;
+      w.x = acc[(c0 + 0) % VT][(c0 + 0) / VT] * vsc[c0 + 0];
+      w.y = acc[(c0 + 1) % VT][(c0 + 1) / VT] * vsc[c0 + 1];
+      w.z = acc[(c0 + 2) % VT][(c0 + 2) / VT] * vsc[c0 + 2];
+      w.w = acc[(c0 + 3) % VT][(c0 + 3) / VT] * vsc[c0 + 3];
+      reinterpret_cast<float4*>(sp)[u] = w;
     }
   }
 }
 
-// Merge split partials (reference kvq/cuda/int8_kv.cu:465-503):
-//   o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30). One wavefront per (token, q head):
-// lane s holds split s's weight; lanes own D / 64 channels each.
+// Merge the split partials of the requests that used more than one split (reference
+// kvq/cuda/int8_kv.cu:465-503): o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30).
+// One wavefront per (request, q head, query token); lane s holds split s's weight; lanes own D / 64
+// channels each.
 template <int D>
-__global__ __launch_bounds__(WAVE) void split_reduce_kernel(uint16_t* __restrict__ out, int64_t o_st, int64_t o_sh,
-                                                            const float* __restrict__ segm_out,
-                                                            const float* __restrict__ segm_max,
-                                                            const float* __restrict__ segm_sum, int64_t seg_st,
-                                                            int64_t seg_sh, const int* __restrict__ cu_q, int S,
-                                                            int qmax) {
+__global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
   const int seq = blockIdx.x, h = blockIdx.y, r = blockIdx.z, lane = threadIdx.x;
-  const int tok = cu_q[seq], qlen = cu_q[seq + 1] - tok;
-  if (qlen == 0 || qlen > qmax || r >= qlen) return;
-  const int64_t base = (int64_t)(tok + r) * seg_st + (int64_t)h * seg_sh;
-  const float ms = lane < S ? segm_max[base + lane] : -INFINITY;
+  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
+  if (qlen == 0 || qlen > a.qmax || r >= qlen) return;
+  const int ntiles = (a.seq_lens[seq] + TILE - 1) / TILE;
+  const int per = split_len(a, ntiles, lane);
+  const int S = ntiles > 0 ? (ntiles + per - 1) / per : 1;
+  if (S <= 1) return;  // written directly by the attention kernel
+  const int64_t base = (int64_t)(tok + r) * a.seg_st + (int64_t)h * a.seg_sh;
+  const float ms = lane < S ? a.segm_max[base + lane] : -INFINITY;
   const float M = wave_max(ms);
   const float w = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-  const float den = wave_sum(lane < S ? w * segm_sum[base + lane] : 0.f);
+  const float den = wave_sum(lane < S ? w * a.segm_sum[base + lane] : 0.f);
   const float inv = 1.f / __builtin_fmaxf(den, 1e-30f);
   constexpr int CPL = D / WAVE;
   float num[CPL];
@@ -540,11 +567,11 @@ __global__ __launch_bounds__(WAVE) void split_reduce_kernel(uint16_t* __restrict
   for (int e = 0; e < CPL; ++e) num[e] = 0.f;
   for (int s = 0; s < S; ++s) {
     const float ws = __shfl(w, s, WAVE);
-    const float* p = segm_out + (base + s) * D + CPL * lane;
+    const float* p = a.segm_out + (base + s) * D + CPL * lane;
 #pragma unroll
     for (int e = 0; e < CPL; ++e) num[e] = __builtin_fmaf(ws, p[e], num[e]);
   }
-  uint16_t* op = out + (int64_t)(tok + r) * o_st + (int64_t)h * o_sh + CPL * lane;
+  uint16_t* op = a.out + (int64_t)(tok + r) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
   if constexpr (CPL == 2) {
     *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(num[0] * inv, num[1] * inv);
   } else {
@@ -553,9 +580,29 @@ __global__ __launch_bounds__(WAVE) void split_reduce_kernel(uint16_t* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------
-// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542). One block per
-// output page (grid stride), 16 channels per lane: a 16-byte int8 load, two 16-byte bf16 stores.
+// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542). Blocks walk
+// the output pages with a grid stride; a lane converts 16 channels of one (token, head): a 16-byte
+// int8 load, two 16-byte bf16 stores (v_cvt_pk_bf16_f32, round to nearest even). When the lanes of
+// a token divide the block, each lane keeps its (head, channels) and their scales for the launch.
 // ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ float i8f(uint32_t w, int b) { return (float)(int8_t)(w >> (8 * b)); }
+
+__device__ __forceinline__ u32x4 dq8(uint32_t w0, uint32_t w1, const float* s) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  u32x4 o;
+  uint32_t r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = j < 2 ? w0 : w1;
+    bf2 h;
+    h.x = (__bf16)(i8f(w, 2 * (j & 1)) * s[2 * j]);
+    h.y = (__bf16)(i8f(w, 2 * (j & 1) + 1) * s[2 * j + 1]);
+    r[j] = *reinterpret_cast<uint32_t*>(&h);
+  }
+  o.x = r[0]; o.y = r[1]; o.z = r[2]; o.w = r[3];
+  return o;
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void dequant_pages_kernel(
     const int8_t* __restrict__ kc, int64_t k_sb, int64_t k_sn, int64_t k_sh, const int8_t* __restrict__ vc,
@@ -564,32 +611,32 @@ __global__ __launch_bounds__(256) void dequant_pages_kernel(
     const int* __restrict__ src_j, int P, const float* __restrict__ ks, int ks_pc, const float* __restrict__ vs,
     int vs_pc) {
   constexpr int CPL = 16, LPR = D / CPL;
-  const int items = bs * H * LPR;
+  const int ipt = H * LPR;                       // lanes per token
+  const int items = bs * ipt;
+  const bool fixed = (int)blockDim.x % ipt == 0;  // lane role invariant across items
+  float kS[CPL], vS[CPL];
+  auto load_scales = [&](int h, int d0) {
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      kS[e] = ks[ks_pc ? h * D + d0 + e : h];
+      vS[e] = vs[vs_pc ? h * D + d0 + e : h];
+    }
+  };
+  if (fixed) load_scales((threadIdx.x % ipt) / LPR, (threadIdx.x % LPR) * CPL);
   for (int p = blockIdx.x; p < P; p += gridDim.x) {
     int src = bt[(int64_t)src_req[p] * bt_stride + src_j[p]];
     if (src < 0 || src >= num_blocks) src = 0;
     for (int it = threadIdx.x; it < items; it += blockDim.x) {
-      const int c = it % LPR, h = (it / LPR) % H, tkn = it / (H * LPR);
+      const int c = it % LPR, h = (it / LPR) % H, tkn = it / ipt;
       const int d0 = c * CPL;
-      const u32x4 kr = *reinterpret_cast<const u32x4*>(kc + (int64_t)src * k_sb + tkn * k_sn + h * k_sh + d0);
-      const u32x4 vr = *reinterpret_cast<const u32x4*>(vc + (int64_t)src * v_sb + tkn * v_sn + h * v_sh + d0);
-      const uint32_t kw[4] = {kr.x, kr.y, kr.z, kr.w}, vw[4] = {vr.x, vr.y, vr.z, vr.w};
-      uint32_t ok[8], ov[8];
-#pragma unroll
-      for (int e = 0; e < CPL; e += 2) {
-        const int ch = h * D + d0 + e;
-        const float k0 = (float)(int8_t)(kw[e / 4] >> (8 * (e % 4)));
-        const float k1 = (float)(int8_t)(kw[e / 4] >> (8 * (e % 4 + 1)));
-        const float v0 = (float)(int8_t)(vw[e / 4] >> (8 * (e % 4)));
-        const float v1 = (float)(int8_t)(vw[e / 4] >> (8 * (e % 4 + 1)));
-        ok[e / 2] = pack_bf16x2(k0 * ks[ks_pc ? ch : h], k1 * ks[ks_pc ? ch + 1 : h]);
-        ov[e / 2] = pack_bf16x2(v0 * vs[vs_pc ? ch : h], v1 * vs[vs_pc ? ch + 1 : h]);
-      }
+      if (!fixed) load_scales(h, d0);
+      const u32x4 kr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kc + (int64_t)src * k_sb + tkn * k_sn + h * k_sh + d0));
+      const u32x4 vr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + (int64_t)src * v_sb + tkn * v_sn + h * v_sh + d0));
       const int64_t o = (((int64_t)p * bs + tkn) * H + h) * D + d0;
-      reinterpret_cast<u32x4*>(ko + o)[0] = u32x4{ok[0], ok[1], ok[2], ok[3]};
-      reinterpret_cast<u32x4*>(ko + o)[1] = u32x4{ok[4], ok[5], ok[6], ok[7]};
-      reinterpret_cast<u32x4*>(vo + o)[0] = u32x4{ov[0], ov[1], ov[2], ov[3]};
-      reinterpret_cast<u32x4*>(vo + o)[1] = u32x4{ov[4], ov[5], ov[6], ov[7]};
+      __builtin_nontemporal_store(dq8(kr.x, kr.y, kS), reinterpret_cast<u32x4*>(ko + o));
+      __builtin_nontemporal_store(dq8(kr.z, kr.w, kS + 8), reinterpret_cast<u32x4*>(ko + o) + 1);
+      __builtin_nontemporal_store(dq8(vr.x, vr.y, vS), reinterpret_cast<u32x4*>(vo + o));
+      __builtin_nontemporal_store(dq8(vr.z, vr.w, vS + 8), reinterpret_cast<u32x4*>(vo + o) + 1);
     }
   }
 }
@@ -627,6 +674,16 @@ int log2i(int64_t x) {
   while ((int64_t(1) << r) < x) ++r;
   return r;
 }
+// Register tiles per wavefront in the attention ring (2..4; KVQ_PREFETCH overrides the default).
+int prefetch_depth() {
+  static const int depth = [] {
+    const char* e = getenv("KVQ_PREFETCH");
+    const int v = e ? atoi(e) : DEFAULT_PREFETCH;
+    return v < 2 ? 2 : (v > 8 ? 8 : v);
+  }();
+  return depth;
+}
+
 int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
@@ -634,10 +691,6 @@ int device_cus() {
   return cus;
 }
 
-template <int D, int NRT>
-void launch_attn(dim3 grid, hipStream_t st, const AttnArgs& a) {
-  hipLaunchKernelGGL((attn_kernel<D, NRT>), grid, dim3(WAVE), 0, st, a);
-}
 
 }  // namespace
 
@@ -651,7 +704,7 @@ int kvq_set_attention_events(void* start, void* stop) {
   return KVQ_OK;
 }
 
-int kvq_abi_version(void) { return 1; }
+int kvq_abi_version(void) { return 2; }
 
 int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
                     int64_t val_sh, int8_t* k_cache, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh, int8_t* v_cache,
@@ -673,8 +726,8 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
   if (n_tokens > INT32_MAX) return fail("quant_cache: too many tokens");
   const int H = (int)num_heads;
   const int ipt = H * (int)(head_dim / QC_CPL), tpb = QC_BLOCK / ipt;
-  const int64_t want = (n_tokens + tpb - 1) / tpb;
-  const int grid = (int)std::min<int64_t>(want, (int64_t)device_cus() * 4);
+  const int64_t want = (n_tokens + (int64_t)tpb * QC_UNROLL - 1) / ((int64_t)tpb * QC_UNROLL);
+  const int grid = (int)std::min<int64_t>(want, (int64_t)device_cus() * 16);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int lbs = log2i(block_size);
   const int64_t num_slots = num_blocks * block_size;
@@ -720,13 +773,13 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               int64_t num_q_heads, const float* k_scale, int64_t k_scale_cols, const float* v_scale,
                               int64_t v_scale_cols, double softmax_scale, float* segm_out, float* segm_max,
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
-                              int64_t max_query_len, int64_t qmax, void* stream) {
+                              int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("int8_decode_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("int8_decode_attention: block_size must be a power of two >= 16");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
     return fail("int8_decode_attention: bad head counts Hq=%lld Hkv=%lld", (long long)num_q_heads, (long long)num_kv_heads);
   if (num_splits < 1 || num_splits > MAX_SPLITS) return fail("int8_decode_attention: at most %d split-KV segments", MAX_SPLITS);
-  if (num_seqs < 0 || max_query_len < 0 || qmax < 1) return fail("int8_decode_attention: bad sizes");
+  if (num_seqs < 0 || max_query_len < 0 || qmax < 1 || target_waves < 0) return fail("int8_decode_attention: bad sizes");
   if (num_seqs == 0) { g_err.clear(); return KVQ_OK; }
   if ((k_scale_cols != 1 && k_scale_cols != head_dim) || (v_scale_cols != 1 && v_scale_cols != head_dim))
     return fail("int8_decode_attention: scale columns must be 1 or head_dim");
@@ -738,9 +791,9 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
     return fail("int8_decode_attention: page too large for 32-bit lane offsets");
   const int G = (int)(num_q_heads / num_kv_heads);
   const int64_t maxq = std::min<int64_t>(std::max<int64_t>(max_query_len, 1), qmax);
-  const int64_t rows = (int64_t)G * maxq;
-  const int nrt = (int)std::min<int64_t>(MAX_ROW_TILES, (rows + 15) / 16);
-  const int64_t row_groups = (rows + 16 * nrt - 1) / (16 * nrt);
+  const int64_t row_tiles = ((int64_t)G * maxq + 15) / 16;
+  const int waves = (int)std::min<int64_t>(MAX_ROW_TILES, row_tiles);
+  const int64_t row_groups = (row_tiles + waves - 1) / waves;
   if (num_seqs > INT32_MAX || num_kv_heads > 65535 || row_groups * num_splits > 65535)
     return fail("int8_decode_attention: grid too large");
   AttnArgs a;
@@ -752,39 +805,37 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.k_sb = k_sb; a.k_sn = k_sn; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sn = v_sn; a.v_sh = v_sh;
   a.seg_st = seg_st; a.seg_sh = seg_sh; a.bt_stride = bt_stride;
   a.sm_log2 = (float)(softmax_scale * 1.4426950408889634);
-  a.num_blocks = (int)num_blocks; a.lbs = log2i(block_size); a.G = G; a.num_splits = (int)num_splits;
-  a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX); a.row_groups = (int)row_groups;
+  a.num_blocks = (int)num_blocks; a.lbs = log2i(block_size); a.G = G;
+  a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX);
   a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
+  a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
+  a.max_splits = (int)num_splits; a.row_tiles = (int)row_tiles; a.waves = waves;
+  a.min_tiles = MIN_SPLIT_TILES;
+  a.target_waves = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)num_seqs, (unsigned)num_kv_heads, (unsigned)(num_splits * row_groups));
   hipEvent_t ev0 = g_ev_start, ev1 = g_ev_stop;
   g_ev_start = g_ev_stop = nullptr;
   if (ev0) (void)hipEventRecord(ev0, st);
+  const dim3 block(WAVE * waves);
+  const int pf = prefetch_depth();
   if (head_dim == 128) {
-    switch (nrt) {
-      case 1: launch_attn<128, 1>(grid, st, a); break;
-      case 2: launch_attn<128, 2>(grid, st, a); break;
-      case 3: launch_attn<128, 3>(grid, st, a); break;
-      default: launch_attn<128, 4>(grid, st, a); break;
-    }
+    if (pf == 2) hipLaunchKernelGGL((attn_kernel<128, 2>), grid, block, 0, st, a);
+    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3>), grid, block, 0, st, a);
+    else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6>), grid, block, 0, st, a);
+    else if (pf == 8) hipLaunchKernelGGL((attn_kernel<128, 8>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_kernel<128, 4>), grid, block, 0, st, a);
   } else {
-    switch (nrt) {
-      case 1: launch_attn<64, 1>(grid, st, a); break;
-      case 2: launch_attn<64, 2>(grid, st, a); break;
-      case 3: launch_attn<64, 3>(grid, st, a); break;
-      default: launch_attn<64, 4>(grid, st, a); break;
-    }
+    if (pf == 2) hipLaunchKernelGGL((attn_kernel<64, 2>), grid, block, 0, st, a);
+    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((attn_kernel<64, 4>), grid, block, 0, st, a);
   }
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);
   if (rc != KVQ_OK || num_splits == 1) return rc;
   const dim3 rgrid((unsigned)num_seqs, (unsigned)num_q_heads, (unsigned)maxq);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE), 0, st, (uint16_t*)out, o_st, o_sh, segm_out, segm_max,
-                       segm_sum, seg_st, seg_sh, cu_seqlens_q, (int)num_splits, a.qmax);
-  else
-    hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE), 0, st, (uint16_t*)out, o_st, o_sh, segm_out, segm_max,
-                       segm_sum, seg_st, seg_sh, cu_seqlens_q, (int)num_splits, a.qmax);
+  if (head_dim == 128) hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE), 0, st, a);
+  else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE), 0, st, a);
   return launched("split_reduce");
 }
 
@@ -803,7 +854,7 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 16)
     return fail("dequant_pages: rows must be 16-byte aligned (base pointers and strides)");
   if (num_pages > INT32_MAX || num_blocks > INT32_MAX) return fail("dequant_pages: too many pages");
-  const int grid = (int)std::min<int64_t>(num_pages, (int64_t)device_cus() * 16);
+  const int grid = (int)std::min<int64_t>(num_pages, (int64_t)device_cus() * 8);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -21,7 +21,7 @@ SIGNATURES = {
     "kvq_quant_q": [_ptr, _i64, _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _ptr, _ptr],
     "kvq_int8_decode_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _i64,
-                                  _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _ptr],
+                                  _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr],
     "kvq_dequant_pages": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
                           _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "kvq_set_attention_events": [_ptr, _ptr],

@@ -156,8 +156,8 @@ class _Ext:
                      seq_lens.data_ptr(), block_table.data_ptr(), block_table.stride(0), num_seqs, Hq,
                      ks.data_ptr(), kcols, vs.data_ptr(), vcols, float(softmax_scale),
                      segm_out.data_ptr() if split else None, segm_max.data_ptr() if split else None,
-                     segm_sum.data_ptr() if split else None, seg_st, seg_sh, S, int(max_query_len), int(qmax),
-                     _stream(q))
+                     segm_sum.data_ptr() if split else None, seg_st, seg_sh, S, _target_waves(),
+                     int(max_query_len), int(qmax), _stream(q))
 
     # kvq/cuda/int8_kv.cu:650-672
     def dequant_pages(self, kc, vc, ko, vo, block_table, src_req, src_j, ks, vs):
@@ -204,25 +204,24 @@ def quant_q(q, k_scale, group=None):
     return tuple(ext().quant_q(q, k_scale, group or q.shape[-1]))
 
 
-def _num_cus(device):
-    return torch.cuda.get_device_properties(device).multi_processor_count
+MIN_SPLIT_KEYS = 128   # the kernels never cut a split shorter than 4 tiles of 32 keys
 
 
-def choose_splits(num_seqs, num_kv_heads, num_q_heads, max_query_len, max_context, num_cus, qmax=None):
-    """Split count for a batch when the caller passes no split buffers: enough wavefronts to cover
-    the GPU (about 8 per compute unit) while every split keeps at least 8 tiles of 32 keys.
-    KVQ_SPLITS overrides it. Pure function of host-side shapes, so a captured graph and the eager
-    call pick the same value."""
+def choose_splits(max_context, num_seqs=None, num_kv_heads=None, num_q_heads=None, max_query_len=1, num_cus=None):
+    """Most splits per request for a batch whose caller passes no split buffers (the kernel then uses,
+    per request, only as many as its length and the batch's total work call for -- see
+    include/kvq_int8.h): enough for the longest possible context (block-table width x block size)
+    to be cut into ranges of 128 keys, at most 64. KVQ_SPLITS overrides it (1 = never split). A pure
+    function of host-side shapes, so a captured graph and the eager call agree."""
     env = os.environ.get("KVQ_SPLITS")
     if env:
         return max(1, min(MAX_SPLITS, int(env)))
-    qmax = SHORT_Q if qmax is None else qmax
-    rows = (num_q_heads // max(num_kv_heads, 1)) * max(1, min(max_query_len, qmax))
-    row_groups = -(-rows // 64)
-    units = max(1, num_seqs * num_kv_heads * row_groups)
-    tiles = -(-max(max_context, 1) // 32)
-    want = -(-8 * num_cus // units)
-    return int(max(1, min(MAX_SPLITS, want, tiles // 8)))
+    return int(max(1, min(MAX_SPLITS, -(-max(max_context, 1) // MIN_SPLIT_KEYS))))
+
+
+def _target_waves():
+    """Wavefronts the kernel spreads a batch over (KVQ_TARGET_WAVES; 0 = the library's 8 per CU)."""
+    return int(os.environ.get("KVQ_TARGET_WAVES", "0"))
 
 
 def decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, softmax_scale, static,
@@ -230,12 +229,12 @@ def decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_tab
     """INT8 attention for the requests with at most SHORT_Q query tokens (others are skipped).
     max_query_len bounds the short queries' length (reference kvq/cuda_kernels.py:51-58).
 
-    segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) splits every context in
-    S ranges (as the reference). Without it the split count is chosen from the shapes
-    (choose_splits) and the partial buffers come from torch's allocator when S > 1."""
+    segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) allows up to S splits per
+    request (the reference always uses S); the kernel gives each request as many of them as its share
+    of the batch's work calls for. Without segm the cap comes from the shapes (choose_splits) and the
+    partial buffers from torch's allocator."""
     if segm is None and cu_seqlens_q.shape[0] > 1:
-        S = choose_splits(cu_seqlens_q.shape[0] - 1, k_cache.shape[2], q.shape[1], max_query_len,
-                          block_table.shape[1] * k_cache.shape[1], _num_cus(q.device))
+        S = choose_splits(block_table.shape[1] * k_cache.shape[1])
         if S > 1:
             T, Hq, D = q.shape
             segm = (torch.empty(T, Hq, S, D, dtype=torch.float32, device=q.device),

@@ -46,7 +46,7 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc == 0 and lib.kvq_last_error() == b""
     # block size 24
     args = [nul, 0, 0, nul, 0, 0, 0, nul, 0, 0, 0, 64, 24, 4, 128, nul, 0, 0, nul, nul, nul, 0, 1, 28, nul, 128, nul,
-            128, 0.1, nul, nul, nul, 0, 0, 1, 1, 8, nul]
+            128, 0.1, nul, nul, nul, 0, 0, 1, 0, 1, 8, nul]
     assert lib.kvq_int8_decode_attention(*args) == 1 and b"power of two" in lib.kvq_last_error()
     args[12] = 16
     args[34] = 65                      # num_splits
@@ -142,16 +142,13 @@ def test_check_inputs_plan_coverage():
 
 # ------------------------------------------------------------ split heuristic
 def test_choose_splits():
-    # headline: 128 requests x 4 kv heads on 256 CUs -> enough splits to give ~8 wavefronts per CU
-    assert ck.choose_splits(128, 4, 28, 1, 32768, 256) == 4
-    # one long request: capped at 64
-    assert ck.choose_splits(1, 4, 28, 1, 32768, 256) == 64
-    # short contexts keep >= 8 tiles per split
-    assert ck.choose_splits(1, 4, 28, 1, 512, 256) == 2
-    assert ck.choose_splits(256, 8, 32, 1, 64, 256) == 1
+    """Cap on splits per request: contexts cut into >= 128-key ranges, at most 64."""
+    assert ck.choose_splits(32768) == 64
+    assert ck.choose_splits(512) == 4
+    assert ck.choose_splits(100) == 1 and ck.choose_splits(0) == 1
     os.environ["KVQ_SPLITS"] = "3"
     try:
-        assert ck.choose_splits(128, 4, 28, 1, 32768, 256) == 3
+        assert ck.choose_splits(32768) == 3
     finally:
         del os.environ["KVQ_SPLITS"]
 
