@@ -45,6 +45,7 @@ constexpr int MAX_ROW_TILES = 4;  // row tiles (wavefronts) per attention workgr
 constexpr int MIN_SPLIT_TILES = 4;  // shortest split: 4 tiles = 128 keys
 constexpr int DEFAULT_WAVES_PER_CU = 8;
 constexpr int DEFAULT_PREFETCH = 3;
+constexpr int NUM_XCDS = 8;
 
 // ------------------------------------------------------------------------------------------------
 // Scalar helpers
@@ -70,15 +71,15 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
 }
 
 // Code of x / s: rint of the correctly rounded fp32 quotient, saturated to [-127, 127]
-// (kvq/quant.py:50-51). r is v_rcp_f32(s) (<= 1 ulp), so q0 = x * r is within |q0| * 2^-22 of
-// fl(x / s); when q0 is farther than |q0| * 2^-19 from every half-integer, rint(q0) equals
-// rint(fl(x / s)). `bad` is set for the rare element that needs the exact division instead.
-// |q0| >= 128 saturates either way.
+// (kvq/quant.py:50-51). r = fl(1 / s) (IEEE division, once per channel), so q0 = fl(x * r) is within
+// |q0| * 1.6 * 2^-23 of fl(x / s); when q0 is farther than |q0| * 2^-21 from every half-integer,
+// rint(q0) equals rint(fl(x / s)). `bad` is set for the rare element that needs the exact division
+// instead. |q0| >= 128 saturates either way.
 __device__ __forceinline__ float code_fast(float x, float r, bool& bad) {
   const float q0 = x * r;
   const float n = __builtin_rintf(q0);
   const float aq = __builtin_fabsf(q0);
-  bad |= (__builtin_fabsf(q0 - n) >= __builtin_fmaf(aq, -0x1p-19f, 0.5f)) & (aq < 128.f);
+  bad |= (__builtin_fabsf(q0 - n) >= __builtin_fmaf(aq, -0x1p-21f, 0.5f)) & (aq < 128.f);
   return sat127(n);
 }
 __device__ __forceinline__ float code_exact(float x, float s) { return sat127(__builtin_rintf(x / s)); }
@@ -97,22 +98,34 @@ __device__ __forceinline__ float wave_sum(float x) {
 // ------------------------------------------------------------------------------------------------
 // Fused quantize + reshape_and_cache (reference kvq/cuda/int8_kv.cu:55-84).
 // A wavefront covers whole tokens: each lane owns 8 channels of one head for the whole launch (their
-// reciprocal scales and K means stay in registers), so a token's K and V rows are read as 1 KB
+// scales, reciprocals and K means stay in registers), so a token's K and V rows are read as 1 KB
 // contiguous runs (H = 4, D = 128) and each (token, head) writes its 128-byte K and V code rows with
-// 16 consecutive lanes -- the 256-byte K|V run of a slot in vLLM's interleaved layout. Every lane
-// issues the loads of QC_UNROLL tokens before converting any of them.
+// 16 consecutive lanes -- the 256-byte K|V run of a slot in vLLM's interleaved layout. Each lane walks
+// its tokens with a ring of QC_PF tokens of loads in flight.
+//
+// Codes: q0 = fl(x * r) with r = v_rcp_f32(s) (<= 1 ulp) is within 2^-22 * |q0| (<= 3.1e-5 for
+// |q0| <= 127.5) of fl(x / s). c = clamp(q0, +-127); t = fl(c + 1.5 * 2^23) holds rint(c) in its low mantissa bits,
+// so the code byte is read straight out of t, and the residual c - (t - 1.5 * 2^23) (exact) tells how
+// close c is to a rounding boundary. Lanes with a residual >= 0.5 - 2^-14 (6.1e-5, 2x the bound)
+// redo their 8 channels with IEEE division; below it rint(fl(x / s)) = rint(q0). Clamping first is
+// exact: rint(clamp(q, +-127)) = clamp(rint(q), +-127), and |q0| > 127 saturates either way.
 // ------------------------------------------------------------------------------------------------
 constexpr int QC_CPL = 8;     // channels per lane
-constexpr int QC_UNROLL = 4;  // tokens per lane and step
+constexpr int QC_PF = 5;      // ring of token loads per lane (QC_PF - 1 in flight ahead)
 constexpr int QC_BLOCK = 256;
+constexpr float QC_MAGIC = 12582912.0f;  // 1.5 * 2^23
 
-// Codes of 8 channels (one 16-byte bf16 run) packed little endian into 2 dwords; K subtracts mu.
-// Fast path with v_rcp reciprocals; a lane whose quotient lies near a rounding boundary redoes its
-// 8 channels with IEEE division (scales re-read from memory).
+// code bytes (little endian) of 4 values t = fl(c + QC_MAGIC)
+__device__ __forceinline__ uint32_t pack_magic4(float t0, float t1, float t2, float t3) {
+  const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(t1), __float_as_uint(t0), 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(t3), __float_as_uint(t2), 0x04000c0cu);
+  return lo | hi;
+}
+
 template <bool SUB_MU>
-__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const float (&mu)[QC_CPL],
-                                        const float* __restrict__ s, int s_pc) {
-  float x[QC_CPL], c[QC_CPL];
+__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const float (&sc)[QC_CPL],
+                                        const float (&mu)[QC_CPL]) {
+  float x[QC_CPL], t[QC_CPL];
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -123,14 +136,19 @@ __device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const
 #pragma unroll
     for (int e = 0; e < QC_CPL; ++e) x[e] = x[e] - mu[e];
   }
-  bool bad = false;
+  float worst = 0.f;
 #pragma unroll
-  for (int e = 0; e < QC_CPL; ++e) c[e] = code_fast(x[e], r[e], bad);
-  if (bad) {
-#pragma unroll
-    for (int e = 0; e < QC_CPL; ++e) c[e] = code_exact(x[e], s[s_pc ? e : 0]);
+  for (int e = 0; e < QC_CPL; ++e) {
+    const float c = sat127(x[e] * r[e]);
+    t[e] = c + QC_MAGIC;
+    const float res = c - (t[e] - QC_MAGIC);
+    worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
   }
-  return u32x2{pack_i8x4(c[0], c[1], c[2], c[3]), pack_i8x4(c[4], c[5], c[6], c[7])};
+  if (worst >= 0.5f - 0x1p-14f) {  // rare: a quotient near a half-integer -- redo this lane exactly
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) t[e] = code_exact(x[e], sc[e]) + QC_MAGIC;
+  }
+  return u32x2{pack_magic4(t[0], t[1], t[2], t[3]), pack_magic4(t[4], t[5], t[6], t[7])};
 }
 
 template <int D>
@@ -146,37 +164,46 @@ __global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
   if ((int)threadIdx.x >= tpb * ipt) return;
   const int item = threadIdx.x % ipt;
   const int h = item / LPH, d0 = (item % LPH) * QC_CPL;
-  const float* ksp = ks + (ks_pc ? h * D + d0 : h);
-  const float* vsp = vs + (vs_pc ? h * D + d0 : h);
-  float kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
-#pragma unroll
-  for (int e = 0; e < QC_CPL; ++e) {
-    kr[e] = __builtin_amdgcn_rcpf(ksp[ks_pc ? e : 0]);
-    vr[e] = __builtin_amdgcn_rcpf(vsp[vs_pc ? e : 0]);
-    mu[e] = kmu[h * D + d0 + e];
-  }
   const int64_t bmask = (int64_t(1) << lbs) - 1;
   const int stride = gridDim.x * tpb;
-  for (int t0 = blockIdx.x * tpb + threadIdx.x / ipt; t0 < n; t0 += QC_UNROLL * stride) {
-    int64_t slot[QC_UNROLL];
-    u32x4 kin[QC_UNROLL], vin[QC_UNROLL];
+  const int t_first = blockIdx.x * tpb + threadIdx.x / ipt;
+  if (t_first >= n) return;
+  const int steps = (n - 1 - t_first) / stride + 1;  // tokens of this lane: t_first + k * stride
+  int64_t slot[QC_PF];
+  u32x4 kin[QC_PF], vin[QC_PF];
+  auto fetch = [&](int j, int k) {  // k clamped: past the end it re-reads the lane's last token
+    const int t = t_first + min(k, steps - 1) * stride;
+    slot[j] = slots[t];
+    kin[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0));
+    vin[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0));
+  };
+  // scales first, then the first tokens' rows: all in flight before anything waits
+  float kS[QC_CPL], vS[QC_CPL], kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
 #pragma unroll
-    for (int u = 0; u < QC_UNROLL; ++u) {
-      const int t = t0 + u * stride;
-      slot[u] = -1;
-      if (t < n) {
-        slot[u] = slots[t];
-        kin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0));
-        vin[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0));
-      }
-    }
+  for (int e = 0; e < QC_CPL; ++e) {
+    kS[e] = ks[ks_pc ? h * D + d0 + e : h];
+    vS[e] = vs[vs_pc ? h * D + d0 + e : h];
+    mu[e] = kmu[h * D + d0 + e];
+  }
 #pragma unroll
-    for (int u = 0; u < QC_UNROLL; ++u) {
-      if (slot[u] < 0 || slot[u] >= num_slots) continue;   // padding (or out of range): skipped
-      const int64_t blk = slot[u] >> lbs, off = slot[u] & bmask;
-      __builtin_nontemporal_store(quant8<true>(kin[u], kr, mu, ksp, ks_pc),
+  for (int j = 0; j < QC_PF - 1; ++j) fetch(j, j);
+#pragma unroll
+  for (int e = 0; e < QC_CPL; ++e) {
+    kr[e] = __builtin_amdgcn_rcpf(kS[e]);
+    vr[e] = __builtin_amdgcn_rcpf(vS[e]);
+  }
+  for (int k0 = 0; k0 < steps; k0 += QC_PF) {
+#pragma unroll
+    for (int j = 0; j < QC_PF; ++j) {
+      const int k = k0 + j;
+      if (k >= steps) break;
+      fetch((j + QC_PF - 1) % QC_PF, k + QC_PF - 1);
+      const int64_t sl = slot[j];
+      if (sl < 0 || sl >= num_slots) continue;   // padding (or out of range): skipped
+      const int64_t blk = sl >> lbs, off = sl & bmask;
+      __builtin_nontemporal_store(quant8<true>(kin[j], kr, kS, mu),
                                   reinterpret_cast<u32x2*>(kc + blk * kc_sb + off * kc_sn + h * kc_sh + d0));
-      __builtin_nontemporal_store(quant8<false>(vin[u], vr, mu, vsp, vs_pc),
+      __builtin_nontemporal_store(quant8<false>(vin[j], vr, vS, mu),
                                   reinterpret_cast<u32x2*>(vc + blk * vc_sb + off * vc_sn + h * vc_sh + d0));
     }
   }
@@ -232,30 +259,139 @@ struct AttnArgs {
   float sm_log2;      // softmax_scale * log2(e)
   int num_blocks, lbs, G, qmax, ks_pc, vs_pc;
   int num_seqs, hkv;
-  int max_splits;     // splits per request in the grid (an upper bound: requests use what they need)
-  int row_tiles;      // 16-row tiles of (token, q head) rows per (request, kv head)
-  int waves;          // wavefronts per workgroup: consecutive row tiles of one (request, kv head, split)
-  int min_tiles;      // shortest split, in 32-key tiles
-  int64_t target_waves;  // the batch's tiles are spread over about this many wavefronts
+  int max_splits;     // split buffers hold this many pieces per (token, q head); 1 = no split buffers
+  int waves;          // wavefronts per workgroup: consecutive 16-row tiles of one (request, kv head)
+  int workers;        // workgroups of the attention grid
+  int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
+  int xcd_order;      // map workgroups to workers XCD by XCD
 };
 
-// 32-key tiles per split of a request with `ntiles` tiles: at most max_splits splits, and long enough
-// that the whole batch (its tiles x kv heads x row tiles) spreads over about target_waves wavefronts,
-// never shorter than min_tiles. The attention kernel and the merge both evaluate it (one whole
-// wavefront, identical integer arithmetic), so they agree on every request's split count.
-__device__ int split_len(const AttnArgs& a, int ntiles, int lane) {
-  if (a.max_splits == 1) return ntiles > 0 ? ntiles : 1;
-  long long part = 0;
-  for (int r = lane; r < a.num_seqs; r += WAVE) part += (a.seq_lens[r] + TILE - 1) / TILE;
+__device__ __forceinline__ long long uniform64(long long x) {
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)(x & 0xffffffffll));
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)((unsigned long long)x >> 32));
+  return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+// What one request asks of the kernel: its 32-key tiles (at least one) and row groups (of `waves`
+// 16-row tiles of (token, q head) rows per kv head). Requests with q_len outside [1, qmax] ask nothing.
+struct ReqWork {
+  int ntiles, rgroups, tok, qlen;
+};
+__device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
+  ReqWork w{0, 0, 0, 0};
+  w.tok = a.cu_q[r];
+  w.qlen = a.cu_q[r + 1] - w.tok;
+  if (w.qlen <= 0 || w.qlen > a.qmax) return w;
+  w.ntiles = max(1, (a.seq_lens[r] + TILE - 1) / TILE);
+  const int rt = (w.qlen * a.G + 15) / 16;
+  w.rgroups = (rt + a.waves - 1) / a.waves;
+  return w;
+}
+// Length, in work units, of each of the request's (kv head, row group) segments: its tile count, or
+// 1 when segments are never cut (no split buffers).
+__device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
+  return a.max_splits == 1 ? (w.ntiles ? 1 : 0) : w.ntiles;
+}
+
+// The batch as one line of work units: request by request, kv head by kv head, row group by row
+// group. Workgroup w takes units [w * chunk, (w + 1) * chunk) (stream-K): every workgroup gets the
+// same amount of K/V to stream however skewed the request lengths are. chunk is also long enough that
+// no segment is cut into more than max_splits pieces. Both the attention and the merge kernel derive
+// it (whole wavefront, the same integer arithmetic), so they agree on every segment's pieces.
+struct Plan {
+  long long total, chunk;
+};
+__device__ Plan make_plan(const AttnArgs& a, int lane, int before = 0, long long* units_before = nullptr) {
+  long long tot = 0, pre = 0;
+  int nmax = 0;
+  for (int r = lane; r < a.num_seqs; r += WAVE) {
+    const ReqWork w = req_work(a, r);
+    const int len = seg_units(a, w);
+    const long long u = (long long)len * a.hkv * w.rgroups;
+    tot += u;
+    if (r < before) pre += u;
+    nmax = max(nmax, len);
+  }
 #pragma unroll
-  for (int o = 32; o; o >>= 1) part += __shfl_xor(part, o, WAVE);
-  const long long units = part * a.hkv * a.row_tiles;
-  const long long target = (units + a.target_waves - 1) / a.target_waves;
-  const int per = (ntiles + a.max_splits - 1) / a.max_splits;
-  // the reduction leaves every lane with the same value; say so, so that the loop bounds (and the
-  // block-table reads they guard) stay scalar
-  return __builtin_amdgcn_readfirstlane(
-      (int)std::max<long long>(std::max<long long>(per, target), std::max(a.min_tiles, 1)));
+  for (int o = 32; o; o >>= 1) {
+    tot += __shfl_xor(tot, o, WAVE);
+    pre += __shfl_xor(pre, o, WAVE);
+    nmax = max(nmax, __shfl_xor(nmax, o, WAVE));
+  }
+  Plan p;
+  p.total = uniform64(tot);
+  long long c = (p.total + a.workers - 1) / a.workers;
+  if (a.max_splits > 1) {
+    c = max(c, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
+    c = max(c, (long long)a.min_tiles);
+  }
+  p.chunk = uniform64(max(c, 1ll));
+  if (units_before) *units_before = uniform64(pre);  // units of the requests before `before`
+  return p;
+}
+
+// make_plan and the search for the request holding unit `pos0` = worker * chunk, in one pass over the
+// requests (their work is read once; up to PLAN_CACHE * 64 requests stay in registers).
+constexpr int PLAN_CACHE = 4;
+__device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_out, long long& start_out) {
+  long long u[PLAN_CACHE];
+  long long tot = 0;
+  int nmax = 0;
+  for (int c = 0; c * WAVE < a.num_seqs; ++c) {
+    const int r = c * WAVE + lane;
+    long long v = 0;
+    if (r < a.num_seqs) {
+      const ReqWork w = req_work(a, r);
+      const int len = seg_units(a, w);
+      v = (long long)len * a.hkv * w.rgroups;
+      nmax = max(nmax, len);
+    }
+    if (c < PLAN_CACHE) u[c] = v;
+    tot += v;
+  }
+#pragma unroll
+  for (int o = 32; o; o >>= 1) {
+    tot += __shfl_xor(tot, o, WAVE);
+    nmax = max(nmax, __shfl_xor(nmax, o, WAVE));
+  }
+  Plan p;
+  p.total = uniform64(tot);
+  long long ch = (p.total + a.workers - 1) / a.workers;
+  if (a.max_splits > 1) {
+    ch = max(ch, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
+    ch = max(ch, (long long)a.min_tiles);
+  }
+  p.chunk = uniform64(max(ch, 1ll));
+  const long long pos = (long long)worker * p.chunk;
+  long long base = 0;
+  r_out = a.num_seqs;
+  start_out = p.total;
+  for (int c = 0; c * WAVE < a.num_seqs && pos < p.total; ++c) {
+    const int r = c * WAVE + lane;
+    long long v = 0;
+    if (c < PLAN_CACHE) {
+      v = u[c];
+    } else if (r < a.num_seqs) {
+      const ReqWork w = req_work(a, r);
+      v = (long long)seg_units(a, w) * a.hkv * w.rgroups;
+    }
+    long long incl = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const long long y = __shfl_up(incl, o, WAVE);
+      if (lane >= o) incl += y;
+    }
+    const long long ctot = uniform64(__shfl(incl, WAVE - 1, WAVE));
+    if (base + ctot > pos) {
+      const unsigned long long m = __ballot(base + incl > pos);
+      const int idx = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
+      r_out = c * WAVE + idx;
+      start_out = base + uniform64(__shfl(incl - v, idx, WAVE));
+      break;
+    }
+    base += ctot;
+  }
+  return p;
 }
 
 // K/V pages are streamed exactly once per launch: the non-temporal hint keeps them from evicting
@@ -283,38 +419,94 @@ __device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t 
   o3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
-// One wavefront = one 16-row tile of one (request, kv head, split); a workgroup holds `waves`
-// consecutive row tiles of the same (request, kv head, split), which stream the same K/V tiles at
-// the same time (the second and later reads hit L1/L2).
+// One wavefront's share of one piece of a segment: its 16-row tile (rows row0..row0+15 of the
+// (token, q head) rows of kv head kvh) over key tiles [c_begin, c_end) of request seq. The piece is
+// the segment's `part`-th of `nparts`: a whole segment writes bf16 out, a cut one an fp32 partial.
 template <int D, int PF>
-__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+__device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
+                                               int c_begin, int c_end, int part, int nparts, int lane) {
   constexpr int KPL = D / 4;        // K bytes per lane and key
   constexpr int KSTEPS = D / 64;    // x64 MFMAs per 16-key block
   constexpr int VT = D / 16;        // PV channel tiles = V bytes per lane and key
   constexpr int VW = D / 64;        // V dwords per lane and key
-  // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
-  const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  // every argument is the same across the wavefront; make that explicit so that the block-table and
+  // length reads and the loop bounds stay scalar (a vector page-id load would make every tile wait for
+  // all K/V loads in flight)
+  seq = __builtin_amdgcn_readfirstlane(seq);
+  tok = __builtin_amdgcn_readfirstlane(tok);
+  qlen = __builtin_amdgcn_readfirstlane(qlen);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  c_begin = __builtin_amdgcn_readfirstlane(c_begin);
+  c_end = __builtin_amdgcn_readfirstlane(c_end);
+  part = __builtin_amdgcn_readfirstlane(part);
+  nparts = __builtin_amdgcn_readfirstlane(nparts);
   const int n = lane & 15, g = lane >> 4;
-  const int seq = blockIdx.x, kvh = blockIdx.y;
-  const int split = blockIdx.z % a.max_splits, rg = blockIdx.z / a.max_splits;
-  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
   const int G = a.G;
-  const int row0 = (rg * a.waves + wave) * 16;  // first (token, q head) row of this wavefront
-  if (qlen == 0 || qlen > a.qmax || row0 >= qlen * G) return;
   const int L = a.seq_lens[seq];
-  const int ntiles = (L + TILE - 1) / TILE;
-  const int per = split_len(a, ntiles, lane);
-  const int nsplit = ntiles > 0 ? (ntiles + per - 1) / per : 1;
-  if (split >= nsplit) return;
-  const int c_begin = split * per, c_end = min(ntiles, c_begin + per);
+  if (L <= 0) c_end = c_begin;  // no keys (malformed): rows come out 0, nothing is read
   const int* bt = a.block_table + (int64_t)seq * a.bt_stride;
   const int bs = 1 << a.lbs;
 
-  // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
   i32x4 qop[KSTEPS];
   const int R = row0 + n, rtok = R / G, rh = R % G;
   float rs;
   int lim;
+  // every row of this wavefront sees at least keys < lim_lo
+  const int lim_lo = L - qlen + 1 + row0 / G;
+
+  float m = -1e30f, l = 0.f, acc[VT][4];
+#pragma unroll
+  for (int t = 0; t < VT; ++t) acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.f;
+
+  const int8_t* kbase = a.kc + (int64_t)kvh * a.k_sh;
+  const int8_t* vbase = a.vc + (int64_t)kvh * a.v_sh;
+  const int koff = n * (int)a.k_sn + g * KPL;            // lane offset of its K bytes inside a 16-key block
+  const int voff = 4 * g * (int)a.v_sn + n * VT;         // lane offset of its first V row
+  const int vsn = (int)a.v_sn;
+
+  auto page_of = [&](int key) -> int {
+    // a scalar load: the block table is read-only during the launch (constant address space), the
+    // index is uniform; a vector load here would make each tile wait for every K/V load in flight
+    const int idx = __builtin_amdgcn_readfirstlane(key >> a.lbs);
+    const int p = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[idx]);
+    return (p >= 0 && p < a.num_blocks) ? p : 0;
+  };
+  auto load = [&](KVTile<D>& r, int c) {
+    const int n0 = c * TILE, n1 = n0 + 16;
+    const int p0 = page_of(n0);
+    const int p1 = n1 < L ? page_of(n1) : p0;
+    const int o0 = n0 & (bs - 1), o1 = n1 < L ? (n1 & (bs - 1)) : o0;
+    const int8_t* kb0 = kbase + (int64_t)p0 * a.k_sb + (int64_t)o0 * a.k_sn;
+    const int8_t* kb1 = kbase + (int64_t)p1 * a.k_sb + (int64_t)o1 * a.k_sn;
+    const int8_t* vb0 = vbase + (int64_t)p0 * a.v_sb + (int64_t)o0 * a.v_sn;
+    const int8_t* vb1 = vbase + (int64_t)p1 * a.v_sb + (int64_t)o1 * a.v_sn;
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+      r.k[0][s] = ldk(reinterpret_cast<const i32x4*>(kb0 + koff + 16 * s));
+      r.k[1][s] = ldk(reinterpret_cast<const i32x4*>(kb1 + koff + 16 * s));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (VW == 2) {
+        const u32x2 w0 = ldv(reinterpret_cast<const u32x2*>(vb0 + voff + i * vsn));
+        const u32x2 w1 = ldv(reinterpret_cast<const u32x2*>(vb1 + voff + i * vsn));
+        r.v[i][0] = w0.x; r.v[i][1] = w0.y;
+        r.v[4 + i][0] = w1.x; r.v[4 + i][1] = w1.y;
+      } else {
+        r.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb0 + voff + i * vsn));
+        r.v[4 + i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb1 + voff + i * vsn));
+      }
+    }
+  };
+
+  KVTile<D> ring[PF];
+  if (c_begin < c_end) {
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) load(ring[j], min(c_begin + j, c_end - 1));
+  }
+
+  // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
   {
     float x[KPL];
     float amax = 0.f;
@@ -356,50 +548,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     rs = s * (a.ks_pc ? 1.f : a.ks[kvh]) * a.sm_log2;
     lim = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
   }
-  // every row of this wavefront sees at least keys < lim_lo
-  const int lim_lo = L - qlen + 1 + row0 / G;
-
-  float m = -1e30f, l = 0.f, acc[VT][4];
-#pragma unroll
-  for (int t = 0; t < VT; ++t) acc[t][0] = acc[t][1] = acc[t][2] = acc[t][3] = 0.f;
-
-  const int8_t* kbase = a.kc + (int64_t)kvh * a.k_sh;
-  const int8_t* vbase = a.vc + (int64_t)kvh * a.v_sh;
-  const int koff = n * (int)a.k_sn + g * KPL;            // lane offset of its K bytes inside a 16-key block
-  const int voff = 4 * g * (int)a.v_sn + n * VT;         // lane offset of its first V row
-  const int vsn = (int)a.v_sn;
-
-  auto page_of = [&](int key) -> int {
-    int p = bt[key >> a.lbs];
-    return (p >= 0 && p < a.num_blocks) ? p : 0;
-  };
-  auto load = [&](KVTile<D>& r, int c) {
-    const int n0 = c * TILE, n1 = n0 + 16;
-    const int p0 = page_of(n0);
-    const int p1 = n1 < L ? page_of(n1) : p0;
-    const int o0 = n0 & (bs - 1), o1 = n1 < L ? (n1 & (bs - 1)) : o0;
-    const int8_t* kb0 = kbase + (int64_t)p0 * a.k_sb + (int64_t)o0 * a.k_sn;
-    const int8_t* kb1 = kbase + (int64_t)p1 * a.k_sb + (int64_t)o1 * a.k_sn;
-    const int8_t* vb0 = vbase + (int64_t)p0 * a.v_sb + (int64_t)o0 * a.v_sn;
-    const int8_t* vb1 = vbase + (int64_t)p1 * a.v_sb + (int64_t)o1 * a.v_sn;
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      r.k[0][s] = ldk(reinterpret_cast<const i32x4*>(kb0 + koff + 16 * s));
-      r.k[1][s] = ldk(reinterpret_cast<const i32x4*>(kb1 + koff + 16 * s));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if constexpr (VW == 2) {
-        const u32x2 w0 = ldv(reinterpret_cast<const u32x2*>(vb0 + voff + i * vsn));
-        const u32x2 w1 = ldv(reinterpret_cast<const u32x2*>(vb1 + voff + i * vsn));
-        r.v[i][0] = w0.x; r.v[i][1] = w0.y;
-        r.v[4 + i][0] = w1.x; r.v[4 + i][1] = w1.y;
-      } else {
-        r.v[i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb0 + voff + i * vsn));
-        r.v[4 + i][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(vb1 + voff + i * vsn));
-      }
-    }
-  };
 
   auto compute = [&](const KVTile<D>& r, int c) {
     const int n0 = c * TILE;
@@ -482,12 +630,10 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
   // ---- main loop: a ring of PF register tiles, PF - 1 of them in flight while one is computed.
   // Loads are never skipped (past the end they re-read the last tile, an L2 hit), so every wait
-  // in the loop is for exactly the oldest tile. ----
+  // in the loop is for exactly the oldest tile. The first PF - 1 tiles were requested before the q
+  // prologue. ----
   if (c_begin < c_end) {
-    KVTile<D> ring[PF];
     const int c_last = c_end - 1;
-#pragma unroll
-    for (int j = 0; j < PF - 1; ++j) load(ring[j], min(c_begin + j, c_last));
     for (int c0 = c_begin; c0 < c_end; c0 += PF) {
 #pragma unroll
       for (int j = 0; j < PF; ++j) {
@@ -511,7 +657,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int t = 0; t < VT; ++t) vsc[VT * i + t] = a.vs_pc ? a.vs[kvh * D + OPL * g + VT * i + t] : a.vs[kvh];
-  if (nsplit == 1) {
+  if (nparts == 1) {
     const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
     uint32_t o[OPL / 2];
 #pragma unroll
@@ -523,7 +669,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < OPL / 8; ++u) op[u] = u32x4{o[4 * u], o[4 * u + 1], o[4 * u + 2], o[4 * u + 3]};
   } else {
-    const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + split;
+    const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + part;
     if (g == 0) {
       a.segm_max[sidx] = m;
       a.segm_sum[sidx] = l;
@@ -542,36 +688,89 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   }
 }
 
-// Merge the split partials of the requests that used more than one split (reference
-// kvq/cuda/int8_kv.cu:465-503): o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30).
-// One wavefront per (request, q head, query token); lane s holds split s's weight; lanes own D / 64
-// channels each.
+// Stream-K attention: workgroup w walks units [w * chunk, (w + 1) * chunk) of the batch (make_plan),
+// segment by segment; its `waves` wavefronts take consecutive 16-row tiles of each segment and stream
+// the same K/V tiles at the same time (the second and later reads hit L1/L2).
+template <int D, int PF>
+__global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
+  // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
+  const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  // workgroups are dispatched round-robin over the XCDs: give each XCD a contiguous range of workers
+  // (so one XCD's L2 sees whole requests' block-table rows and q); KVQ_XCD_ORDER=0 turns it off
+  int worker = blockIdx.x;
+  if (a.xcd_order) {
+    const int nx = NUM_XCDS, per = (a.workers + nx - 1) / nx;
+    const int wx = blockIdx.x % nx, wi = blockIdx.x / nx;
+    worker = wx * per + wi;
+    if (worker >= a.workers) return;
+  }
+  int r;
+  long long rstart;
+  const Plan pl = plan_and_locate(a, worker, lane, r, rstart);
+  long long pos = (long long)worker * pl.chunk;
+  const long long end = min(pos + pl.chunk, pl.total);
+  if (pos >= end || r >= a.num_seqs) return;
+  ReqWork w = req_work(a, r);
+  int seglen = seg_units(a, w);
+  int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
+  const bool whole = a.max_splits == 1;
+  while (pos < end) {
+    const long long seg_start = rstart + (long long)seg * seglen;
+    const int take = (int)min((long long)(seglen - off), end - pos);
+    const long long first = seg_start / pl.chunk, last = (seg_start + seglen - 1) / pl.chunk;
+    const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
+    const int row0 = (rg * a.waves + wave) * 16;
+    if (row0 < w.qlen * a.G)
+      attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, whole ? 0 : off, whole ? w.ntiles : off + take,
+                            (int)(worker - first), (int)(last - first + 1), lane);
+    pos += take;
+    off = 0;
+    if (++seg == a.hkv * w.rgroups && pos < end) {  // on to the next request with work
+      rstart += (long long)seglen * a.hkv * w.rgroups;
+      seg = 0;
+      do {
+        if (++r >= a.num_seqs) return;
+        w = req_work(a, r);
+      } while (w.ntiles == 0);
+      seglen = seg_units(a, w);
+    }
+  }
+}
+
+// Merge the pieces of the cut segments (reference kvq/cuda/int8_kv.cu:465-503):
+//   o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30)
+// One wavefront per (request, q head, query token); lane s holds piece s's weight; lanes own D / 64
+// channels each. Rows of uncut segments were written by the attention kernel and are skipped.
 template <int D>
 __global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
-  const int seq = blockIdx.x, h = blockIdx.y, r = blockIdx.z, lane = threadIdx.x;
-  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
-  if (qlen == 0 || qlen > a.qmax || r >= qlen) return;
-  const int ntiles = (a.seq_lens[seq] + TILE - 1) / TILE;
-  const int per = split_len(a, ntiles, lane);
-  const int S = ntiles > 0 ? (ntiles + per - 1) / per : 1;
-  if (S <= 1) return;  // written directly by the attention kernel
-  const int64_t base = (int64_t)(tok + r) * a.seg_st + (int64_t)h * a.seg_sh;
+  const int seq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+  const ReqWork w = req_work(a, seq);
+  if (w.ntiles == 0 || t >= w.qlen) return;
+  long long rstart;
+  const Plan pl = make_plan(a, lane, seq, &rstart);
+  const int kvh = h / a.G, row = t * a.G + h % a.G;
+  const int seg = kvh * w.rgroups + (row / 16) / a.waves;
+  const int seglen = seg_units(a, w);
+  const long long seg_start = rstart + (long long)seg * seglen;
+  const int S = (int)((seg_start + seglen - 1) / pl.chunk - seg_start / pl.chunk + 1);
+  if (S <= 1) return;
+  const int64_t base = (int64_t)(w.tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
   const float ms = lane < S ? a.segm_max[base + lane] : -INFINITY;
   const float M = wave_max(ms);
-  const float w = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-  const float den = wave_sum(lane < S ? w * a.segm_sum[base + lane] : 0.f);
+  const float wt = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
+  const float den = wave_sum(lane < S ? wt * a.segm_sum[base + lane] : 0.f);
   const float inv = 1.f / __builtin_fmaxf(den, 1e-30f);
   constexpr int CPL = D / WAVE;
   float num[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) num[e] = 0.f;
   for (int s = 0; s < S; ++s) {
-    const float ws = __shfl(w, s, WAVE);
+    const float ws = __shfl(wt, s, WAVE);
     const float* p = a.segm_out + (base + s) * D + CPL * lane;
 #pragma unroll
     for (int e = 0; e < CPL; ++e) num[e] = __builtin_fmaf(ws, p[e], num[e]);
   }
-  uint16_t* op = a.out + (int64_t)(tok + r) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
+  uint16_t* op = a.out + (int64_t)(w.tok + t) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
   if constexpr (CPL == 2) {
     *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(num[0] * inv, num[1] * inv);
   } else {
@@ -610,33 +809,44 @@ __global__ __launch_bounds__(256) void dequant_pages_kernel(
     uint16_t* __restrict__ vo, const int* __restrict__ bt, int64_t bt_stride, const int* __restrict__ src_req,
     const int* __restrict__ src_j, int P, const float* __restrict__ ks, int ks_pc, const float* __restrict__ vs,
     int vs_pc) {
-  constexpr int CPL = 16, LPR = D / CPL;
-  const int ipt = H * LPR;                       // lanes per token
-  const int items = bs * ipt;
-  const bool fixed = (int)blockDim.x % ipt == 0;  // lane role invariant across items
-  float kS[CPL], vS[CPL];
-  auto load_scales = [&](int h, int d0) {
+  // One wavefront per (output page, head). A token's K and V rows are 2 * D / 16 lanes' worth of
+  // 16-byte runs; lane l keeps the same run position (K or V, channels) for every token it visits,
+  // so its 16 scales are loaded once. All of the lane's loads for the page are issued before any
+  // conversion.
+  constexpr int CPL = 16, RUNS = 2 * D / CPL;   // 16-channel runs per token (K then V)
+  constexpr int TPW = WAVE / RUNS;              // tokens per wavefront pass
+  constexpr int MAXP = 8;                       // passes in flight: block sizes up to TPW * MAXP
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int unit = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+  if (unit >= P * H) return;
+  const int p = unit / H, h = unit % H;
+  const int run = lane % RUNS, t0 = lane / RUNS;
+  const bool is_v = run >= RUNS / 2;
+  const int d0 = (run % (RUNS / 2)) * CPL;
+  float sc[CPL];
+  const float* sp = is_v ? vs : ks;
+  const int pc = is_v ? vs_pc : ks_pc;
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) {
-      kS[e] = ks[ks_pc ? h * D + d0 + e : h];
-      vS[e] = vs[vs_pc ? h * D + d0 + e : h];
+  for (int e = 0; e < CPL; ++e) sc[e] = sp[pc ? h * D + d0 + e : h];
+  int src = bt[(int64_t)src_req[p] * bt_stride + src_j[p]];
+  if (src < 0 || src >= num_blocks) src = 0;
+  const int8_t* base = (is_v ? vc + (int64_t)src * v_sb + (int64_t)h * v_sh : kc + (int64_t)src * k_sb + (int64_t)h * k_sh) + d0;
+  const int64_t tstride = is_v ? v_sn : k_sn;
+  uint16_t* obase = (is_v ? vo : ko) + ((int64_t)p * bs * H + h) * D + d0;
+  for (int tb = 0; tb < bs; tb += TPW * MAXP) {
+    u32x4 w[MAXP];
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+      const int tkn = tb + t0 + i * TPW;
+      if (tkn < bs) w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + tkn * tstride));
     }
-  };
-  if (fixed) load_scales((threadIdx.x % ipt) / LPR, (threadIdx.x % LPR) * CPL);
-  for (int p = blockIdx.x; p < P; p += gridDim.x) {
-    int src = bt[(int64_t)src_req[p] * bt_stride + src_j[p]];
-    if (src < 0 || src >= num_blocks) src = 0;
-    for (int it = threadIdx.x; it < items; it += blockDim.x) {
-      const int c = it % LPR, h = (it / LPR) % H, tkn = it / ipt;
-      const int d0 = c * CPL;
-      if (!fixed) load_scales(h, d0);
-      const u32x4 kr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kc + (int64_t)src * k_sb + tkn * k_sn + h * k_sh + d0));
-      const u32x4 vr = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vc + (int64_t)src * v_sb + tkn * v_sn + h * v_sh + d0));
-      const int64_t o = (((int64_t)p * bs + tkn) * H + h) * D + d0;
-      __builtin_nontemporal_store(dq8(kr.x, kr.y, kS), reinterpret_cast<u32x4*>(ko + o));
-      __builtin_nontemporal_store(dq8(kr.z, kr.w, kS + 8), reinterpret_cast<u32x4*>(ko + o) + 1);
-      __builtin_nontemporal_store(dq8(vr.x, vr.y, vS), reinterpret_cast<u32x4*>(vo + o));
-      __builtin_nontemporal_store(dq8(vr.z, vr.w, vS + 8), reinterpret_cast<u32x4*>(vo + o) + 1);
+#pragma unroll
+    for (int i = 0; i < MAXP; ++i) {
+      const int tkn = tb + t0 + i * TPW;
+      if (tkn >= bs) break;
+      u32x4* o = reinterpret_cast<u32x4*>(obase + (int64_t)tkn * H * D);
+      __builtin_nontemporal_store(dq8(w[i].x, w[i].y, sc), o);
+      __builtin_nontemporal_store(dq8(w[i].z, w[i].w, sc + 8), o + 1);
     }
   }
 }
@@ -726,8 +936,8 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
   if (n_tokens > INT32_MAX) return fail("quant_cache: too many tokens");
   const int H = (int)num_heads;
   const int ipt = H * (int)(head_dim / QC_CPL), tpb = QC_BLOCK / ipt;
-  const int64_t want = (n_tokens + (int64_t)tpb * QC_UNROLL - 1) / ((int64_t)tpb * QC_UNROLL);
-  const int grid = (int)std::min<int64_t>(want, (int64_t)device_cus() * 16);
+  const int64_t want = (n_tokens + tpb - 1) / tpb;
+  const int grid = (int)std::min<int64_t>(want, (int64_t)device_cus() * 4);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int lbs = log2i(block_size);
   const int64_t num_slots = num_blocks * block_size;
@@ -793,9 +1003,7 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   const int64_t maxq = std::min<int64_t>(std::max<int64_t>(max_query_len, 1), qmax);
   const int64_t row_tiles = ((int64_t)G * maxq + 15) / 16;
   const int waves = (int)std::min<int64_t>(MAX_ROW_TILES, row_tiles);
-  const int64_t row_groups = (row_tiles + waves - 1) / waves;
-  if (num_seqs > INT32_MAX || num_kv_heads > 65535 || row_groups * num_splits > 65535)
-    return fail("int8_decode_attention: grid too large");
+  if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535) return fail("int8_decode_attention: grid too large");
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = k_cache; a.vc = v_cache; a.out = (uint16_t*)out;
   a.segm_out = segm_out; a.segm_max = segm_max; a.segm_sum = segm_sum;
@@ -809,11 +1017,13 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX);
   a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
-  a.max_splits = (int)num_splits; a.row_tiles = (int)row_tiles; a.waves = waves;
+  a.max_splits = (int)num_splits; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES;
-  a.target_waves = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
+  a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
+  const int64_t tw = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
+  a.workers = (int)std::max<int64_t>(1, std::min<int64_t>(tw / waves, INT32_MAX));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)num_seqs, (unsigned)num_kv_heads, (unsigned)(num_splits * row_groups));
+  const dim3 grid((unsigned)a.workers);
   hipEvent_t ev0 = g_ev_start, ev1 = g_ev_stop;
   g_ev_start = g_ev_stop = nullptr;
   if (ev0) (void)hipEventRecord(ev0, st);
@@ -854,10 +1064,12 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 16)
     return fail("dequant_pages: rows must be 16-byte aligned (base pointers and strides)");
   if (num_pages > INT32_MAX || num_blocks > INT32_MAX) return fail("dequant_pages: too many pages");
-  const int grid = (int)std::min<int64_t>(num_pages, (int64_t)device_cus() * 8);
+  if (num_pages * num_heads > (int64_t)INT32_MAX * 4 / 5) return fail("dequant_pages: too many pages");
+  const int64_t units = num_pages * num_heads;
+  const int grid = (int)((units + 3) / 4);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(4 * WAVE), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,
                        (int)num_blocks, (int)block_size, (int)num_heads, (uint16_t*)k_out, (uint16_t*)v_out,
                        block_table, bt_stride, src_req, src_j, (int)num_pages, k_scale, (int)(k_scale_cols > 1),
                        v_scale, (int)(v_scale_cols > 1));
