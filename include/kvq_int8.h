@@ -63,13 +63,14 @@ int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, i
  * Replaces the pybind op int8_decode_attention (reference kvq/cuda/int8_kv.cu:600-648, kernels
  * :168-463 and :472-503), bound as kvq/cuda_kernels.py:51-58 decode_attention.
  * Requests with q_len == 0 or q_len > qmax are skipped (their out rows untouched).
- * num_splits == 1: every context in one pass, out written directly, segm_* ignored (may be NULL).
- * num_splits  > 1 (<= 64): the most splits a request may use. Each request's context is cut into
- *   ranges of whole 32-key tiles, as few as spread the batch's tiles over about target_waves
- *   wavefronts (0 = 8 per compute unit), at most num_splits, none under 128 keys. A request left with
- *   one range writes out directly; the others write partials to segm_out [T, Hq, S, D] and
- *   segm_max / segm_sum [T, Hq, S] (fp32; element (t, h, s) at t * seg_st + h * seg_sh + s, segm_out
- *   at that index * D + d), which a second kernel merges. */
+ * Work is split stream-K: the batch is one line of units -- request by request, kv head by kv head,
+ * group of up to four 16-row tiles of (token, q head) rows, then 32-key tile -- and each of about
+ * target_waves / waves_per_group workgroups (0 = 8 wavefronts per compute unit) takes an equal
+ * contiguous range of it. A (request, kv head, row group) that one workgroup covers whole writes out
+ * directly; one that is cut writes fp32 pieces to segm_out [T, Hq, S, D] and segm_max / segm_sum
+ * [T, Hq, S] (element (t, h, s) at t * seg_st + h * seg_sh + s, segm_out at that index * D + d),
+ * which a second kernel merges. num_splits (<= 64) is S, the most pieces the buffers hold: no
+ * segment is cut into more. num_splits == 1: nothing is cut (segm_* may be NULL). */
 int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
                               int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
                               int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,

@@ -884,7 +884,8 @@ int log2i(int64_t x) {
   while ((int64_t(1) << r) < x) ++r;
   return r;
 }
-// Register tiles per wavefront in the attention ring (2..4; KVQ_PREFETCH overrides the default).
+// Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
+// instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
 int prefetch_depth() {
   static const int depth = [] {
     const char* e = getenv("KVQ_PREFETCH");
