@@ -17,6 +17,7 @@ FLAGS = [
     "-ffp-contract=off",                               # every fma in the kernels is written out
     "-fhip-fp32-correctly-rounded-divide-sqrt",        # x / s is IEEE division (bit-exact codes)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",             # MFMA results in VGPRs (no v_accvgpr_read copies)
 ]
 
 

@@ -29,6 +29,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "../../include/kvq_int8.h"
 
@@ -83,6 +84,38 @@ __device__ __forceinline__ float code_fast(float x, float r, bool& bad) {
   return sat127(n);
 }
 __device__ __forceinline__ float code_exact(float x, float s) { return sat127(__builtin_rintf(x / s)); }
+
+// x / 127, correctly rounded, for every float x in [2^-126, 1] (the range of a P tile maximum):
+// q = fl(x * fl(1/127)), the remainder x - 127 q is exact in one FMA, and one more FMA corrects q.
+// Checked against IEEE division for all 2^30 floats of that range on the host (tests/test_arith.py).
+// Below 2^-126 the caller clamps the result to 1e-30 anyway.
+__device__ __forceinline__ float div127(float x) {
+  constexpr float R = 1.f / 127.f;
+  const float q = x * R;
+  return __builtin_fmaf(__builtin_fmaf(-q, 127.f, x), R, q);
+}
+
+// Reductions over the lanes l, l ^ 16, l ^ 32, l ^ 48 -- the four lane groups of one row (or one
+// column) of the 16x16 MFMA layouts -- with the gfx950 lane-swap instructions: each swap leaves the
+// pair {v[l], v[l ^ 32]} (then {v[l], v[l ^ 16]}) in the two results of every lane, no LDS round trip.
+__device__ __forceinline__ int group4_max(int v) {
+  const auto a = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  v = max((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  return max((int)b[0], (int)b[1]);
+}
+__device__ __forceinline__ float group4_fmax(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float group4_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
@@ -531,8 +564,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
 #pragma unroll
       for (int e = 0; e < KPL; ++e) x[e] = 0.f;
     }
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16, WAVE));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, WAVE));
+    amax = group4_fmax(amax);
     const float s = __builtin_fmaxf(amax / 127.f, 1e-8f);
 #pragma unroll
     for (int st = 0; st < KSTEPS; ++st) {
@@ -549,7 +581,10 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     lim = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
   }
 
-  auto compute = [&](const KVTile<D>& r, int c) {
+  // One 32-key tile. MASKED: some key of the tile is at or past some row's limit (the last tiles of
+  // a request, causal rows); other tiles skip the per-key limit test.
+  auto compute = [&](auto masked_t, const KVTile<D>& r, int c) {
+    constexpr bool MASKED = decltype(masked_t)::value;
     const int n0 = c * TILE;
     // ---- QK: S^T[key][row] for the tile's two 16-key blocks ----
     i32x4 sc[2];
@@ -580,37 +615,40 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
       for (int t = 0; t < VT; ++t) vop[t] = (long)(((uint64_t)hi[t] << 32) | lo[t]);
     }
     // ---- online softmax; key of accumulator (b, i) = n0 + 16 b + 4 g + i ----
-    const bool full = n0 + TILE <= lim_lo;  // no key of this tile is masked for any row
     int mx = INT32_MIN;
     bool ok[2][4];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        ok[b][i] = full || n0 + 16 * b + 4 * g + i < lim;
+        ok[b][i] = MASKED ? n0 + 16 * b + 4 * g + i < lim : true;
         mx = ok[b][i] ? max(mx, sc[b][i]) : mx;
       }
-    mx = max(mx, __shfl_xor(mx, 16, WAVE));
-    mx = max(mx, __shfl_xor(mx, 32, WAVE));
-    const float tmax = mx == INT32_MIN ? -INFINITY : (float)mx * rs;
+    mx = group4_max(mx);
+    // an int8 dot product never reaches INT32_MIN: it marks a row with no visible key in the tile
+    const float tmax = (MASKED && mx == INT32_MIN) ? -INFINITY : (float)mx * rs;
     const float mnew = __builtin_fmaxf(m, tmax);
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     m = mnew;
     const float pm = __builtin_amdgcn_exp2f(tmax - mnew);  // max of this tile's P (exp2 is monotone)
-    const float ps = __builtin_fmaxf(pm / 127.f, 1e-30f);
+    const float ps = __builtin_fmaxf(div127(pm), 1e-30f);
     const float ri = __builtin_amdgcn_rcpf(ps);
-    float pc[2][4];
+    // p_i8 = min(rint(P / ps), 127): fl(P * ri + 1.5 * 2^23) rounds to the nearest integer (ties to
+    // even) and holds the code in its low byte; masked keys get code 0
+    float t[2][4];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[b][i], rs, -mnew));
-        pc[b][i] = ok[b][i] ? __builtin_fminf(__builtin_rintf(p * ri), 127.f) : 0.f;
+        const float v = __builtin_fminf(__builtin_fmaf(p, ri, QC_MAGIC), QC_MAGIC + 127.f);
+        t[b][i] = ok[b][i] ? v : QC_MAGIC;
       }
-    const uint32_t p0 = pack_i8x4(pc[0][0], pc[0][1], pc[0][2], pc[0][3]);
-    const uint32_t p1 = pack_i8x4(pc[1][0], pc[1][1], pc[1][2], pc[1][3]);
+    const uint32_t p0 = pack_magic4(t[0][0], t[0][1], t[0][2], t[0][3]);
+    const uint32_t p1 = pack_magic4(t[1][0], t[1][1], t[1][2], t[1][3]);
     const long pop = (long)(((uint64_t)p1 << 32) | p0);
-    const float psum = (pc[0][0] + pc[0][1]) + (pc[0][2] + pc[0][3]) + (pc[1][0] + pc[1][1]) + (pc[1][2] + pc[1][3]);
+    // sum of the 8 codes (v_sad_u8: sum of |byte - 0|)
+    const float psum = (float)__builtin_amdgcn_sad_u8(p1, 0u, __builtin_amdgcn_sad_u8(p0, 0u, 0u));
     l = __builtin_fmaf(psum, ps, l * alpha);
     if (__any(alpha != 1.f)) {
 #pragma unroll
@@ -631,23 +669,33 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   // ---- main loop: a ring of PF register tiles, PF - 1 of them in flight while one is computed.
   // Loads are never skipped (past the end they re-read the last tile, an L2 hit), so every wait
   // in the loop is for exactly the oldest tile. The first PF - 1 tiles were requested before the q
-  // prologue. ----
+  // prologue. Tiles below full_end have no masked key for any row of the wavefront; the first loop
+  // runs whole rounds of them, the second the rest (masked or not) -- both start rounds at
+  // c_begin + k * PF, so the ring slot of every tile is a compile-time index. ----
   if (c_begin < c_end) {
     const int c_last = c_end - 1;
-    for (int c0 = c_begin; c0 < c_end; c0 += PF) {
+    const int full_end = max(c_begin, min(c_end, lim_lo > 0 ? lim_lo / TILE : 0));
+    int c0 = c_begin;
+    for (; c0 + PF <= full_end; c0 += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        load(ring[(j + PF - 1) % PF], min(c0 + j + PF - 1, c_last));
+        compute(std::false_type{}, ring[j], c0 + j);
+      }
+    }
+    for (; c0 < c_end; c0 += PF) {
 #pragma unroll
       for (int j = 0; j < PF; ++j) {
         const int c = c0 + j;
         if (c >= c_end) break;
         load(ring[(j + PF - 1) % PF], min(c + PF - 1, c_last));
-        compute(ring[j], c);
+        compute(std::true_type{}, ring[j], c);
       }
     }
   }
 
   // ---- epilogue: lane (n, g) holds channels (D/4) g + (D/16) i + t of row n ----
-  l += __shfl_xor(l, 16, WAVE);
-  l += __shfl_xor(l, 32, WAVE);
+  l = group4_sum(l);
   if (rtok >= qlen) return;
   constexpr int OPL = D / 4;
   const int head = kvh * G + rh;
@@ -696,14 +744,16 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   // workgroups are dispatched round-robin over the XCDs: give each XCD a contiguous range of workers
-  // (so one XCD's L2 sees whole requests' block-table rows and q); KVQ_XCD_ORDER=0 turns it off
+  // (so one XCD's L2 sees whole requests' block-table rows and q); KVQ_XCD_ORDER=0 turns it off.
+  // XCD x holds the blocks b = x (mod 8), q + (x < rem) of them for W = 8 q + rem, and takes the
+  // workers [x q + min(x, rem), ...) -- consecutive ranges that tile [0, W) exactly.
   int worker = blockIdx.x;
   if (a.xcd_order) {
-    const int nx = NUM_XCDS, per = (a.workers + nx - 1) / nx;
-    const int wx = blockIdx.x % nx, wi = blockIdx.x / nx;
-    worker = wx * per + wi;
-    if (worker >= a.workers) return;
+    const int q = a.workers / NUM_XCDS, rem = a.workers % NUM_XCDS;
+    const int wx = blockIdx.x % NUM_XCDS, wi = blockIdx.x / NUM_XCDS;
+    worker = wx * q + min(wx, rem) + wi;
   }
+  if (worker >= a.workers) return;
   int r;
   long long rstart;
   const Plan pl = plan_and_locate(a, worker, lane, r, rstart);

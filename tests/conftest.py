@@ -24,6 +24,21 @@ def record(test, **metrics):
             f.write(json.dumps({"test": test, **metrics}) + "\n")
 
 
+def nan_like(t):
+    """An output buffer that starts as NaN, so a row a kernel fails to write cannot pass a check."""
+    import torch
+    return torch.full_like(t, float("nan"))
+
+
+def nan_segm(T, H, S, D, device="cuda"):
+    """Split-KV partial buffers (segm_out [T, H, S, D], segm_max / segm_sum [T, H, S]) filled with NaN:
+    a piece that is merged but never written shows up in the output."""
+    import torch
+    nan = float("nan")
+    return (torch.full((T, H, S, D), nan, device=device), torch.full((T, H, S), nan, device=device),
+            torch.full((T, H, S), nan, device=device))
+
+
 @pytest.fixture(scope="session")
 def golden():
     from safetensors.torch import load_file

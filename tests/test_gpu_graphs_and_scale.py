@@ -5,7 +5,7 @@ import os
 
 import pytest
 import torch
-from conftest import record
+from conftest import nan_like, nan_segm, record
 
 from oracle import kvq_oracle as O
 from kvq import cuda_kernels as ck
@@ -47,9 +47,8 @@ def test_replay_matches_eager_with_new_inputs(q_len, split):
     T = d["q"].shape[0]
     segm = None
     if split == "segm16":
-        segm = (torch.empty(T, 28, 16, 128, device=DEV), torch.empty(T, 28, 16, device=DEV),
-                torch.empty(T, 28, 16, device=DEV))
-    out = torch.empty_like(d["q"])
+        segm = nan_segm(T, 28, 16, 128)
+    out = nan_like(d["q"])
 
     def attn(o):
         return ck.decode_attention(d["q"], kq, vq, o, d["cu"], d["seq_lens"], d["block_table"], SCALE, st,
@@ -62,7 +61,7 @@ def test_replay_matches_eager_with_new_inputs(q_len, split):
         d["seq_lens"].add_(1)
         g.replay()
         torch.cuda.synchronize()
-        ref = attn(torch.empty_like(d["q"]))
+        ref = attn(nan_like(d["q"]))
         torch.cuda.synchronize()
         err = O.compare(ref.cpu(), out.cpu())
         record("graph_replay", q_len=q_len, split=split, rep=rep, **err)
@@ -73,7 +72,7 @@ def test_scales_must_be_updated_in_place():
     """tests/test_cudagraph.py:56-84: rebinding a scale tensor does not reach the graph, an in-place
     update does."""
     d, kq, vq, st = _case(1)
-    out = torch.empty_like(d["q"])
+    out = nan_like(d["q"])
     attn = lambda o, s: ck.decode_attention(d["q"], kq, vq, o, d["cu"], d["seq_lens"], d["block_table"], SCALE, s)
     g = _capture(lambda: attn(out, st))
     g.replay()
@@ -83,7 +82,7 @@ def test_scales_must_be_updated_in_place():
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, before)
-    expected = attn(torch.empty_like(d["q"]), rebound)
+    expected = attn(nan_like(d["q"]), rebound)
     assert not torch.allclose(out, expected)
     st["v_scale"].mul_(2)                     # same storage the graph captured
     g.replay()
@@ -150,7 +149,7 @@ def test_c2_full_size_sampled_parity():
     q = torch.randn(B, hq, d, generator=g, device=DEV).to(torch.bfloat16)
     cu = torch.arange(B + 1, dtype=torch.int32, device=DEV)
     sl = torch.full((B,), L, dtype=torch.int32, device=DEV)
-    out = ck.decode_attention(q, kc, vc, torch.empty_like(q), cu, sl, bt, SCALE, st)
+    out = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st)
     for r in (0, 17, 63, 64, 100, 127):
         ref = _request_oracle(kc, vc, bt, r, L, q[r:r + 1], st)
         err = O.compare(ref, out[r:r + 1].cpu())
@@ -158,7 +157,7 @@ def test_c2_full_size_sampled_parity():
         assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (r, err)
     os.environ["KVQ_SPLITS"] = "1"
     try:
-        one = ck.decode_attention(q, kc, vc, torch.empty_like(q), cu, sl, bt, SCALE, st)
+        one = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st)
     finally:
         del os.environ["KVQ_SPLITS"]
     e = O.compare(one.cpu(), out.cpu())
@@ -178,7 +177,7 @@ def test_c3_verification_full_parity():
     ref = O.paged_static_attention(O.CFG32_Q32, st, True, 8)(c["q"].float(), kq, vq, c["cu"], c["seq_lens"],
                                                                c["block_table"], SCALE)
     d = {k: v.to(DEV) for k, v in c.items() if isinstance(v, torch.Tensor)}
-    out = ck.decode_attention(d["q"], kq.to(DEV), vq.to(DEV), torch.empty_like(d["q"]), d["cu"], d["seq_lens"],
+    out = ck.decode_attention(d["q"], kq.to(DEV), vq.to(DEV), nan_like(d["q"]), d["cu"], d["seq_lens"],
                               d["block_table"], SCALE, {k: v.to(DEV) for k, v in st.items()}, max_query_len=8)
     err = O.compare(ref, out.cpu())
     record("c3_full", **err)
@@ -200,7 +199,7 @@ def test_c4_decode_rows_sampled_parity():
     g = torch.Generator(device=DEV).manual_seed(7)
     q = torch.randn(96, hq, d, generator=g, device=DEV).to(torch.bfloat16)
     cu = torch.arange(97, dtype=torch.int32, device=DEV)
-    out = ck.decode_attention(q, kc, vc, torch.empty_like(q), cu, torch.tensor(lens, dtype=torch.int32, device=DEV),
+    out = ck.decode_attention(q, kc, vc, nan_like(q), cu, torch.tensor(lens, dtype=torch.int32, device=DEV),
                               bt, SCALE, st)
     order = sorted(range(96), key=lambda r: lens[r])
     for r in [0, 1, 2] + order[::10]:

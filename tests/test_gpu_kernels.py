@@ -9,7 +9,7 @@ import os
 import numpy as np
 import pytest
 import torch
-from conftest import record
+from conftest import nan_like, nan_segm, record
 
 import cases
 from oracle import c_oracle
@@ -146,7 +146,7 @@ def test_attention_matches_reference_golden(golden, name):
     c = cases.build(name)
     kq, vq = int8_cache(c)
     d = dev(c)
-    out = torch.empty_like(d["q"])
+    out = nan_like(d["q"])
     if name == "mixed":
         plan = ck.plan_long(c["cu"], c["seq_lens"], 16)
         ck.paged_attention(d["q"], dev(kq), dev(vq), out, d["cu"], d["seq_lens"], d["block_table"],
@@ -200,9 +200,8 @@ def test_short_queries_match_oracle(shape, case, variant):
     T = c["q"].shape[0]
     segm = None
     if variant == "segments":
-        segm = (torch.empty(T, hq, 16, d, device=DEV), torch.empty(T, hq, 16, device=DEV),
-                torch.empty(T, hq, 16, device=DEV))
-    out = ck.decode_attention(dc["q"], dev(kq), dev(vq), torch.empty_like(dc["q"]), dc["cu"], dc["seq_lens"],
+        segm = nan_segm(T, hq, 16, d)
+    out = ck.decode_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
                               dc["block_table"], c["scale"], dc["static"], segm=segm, max_query_len=max(q_lens))
     check_attention(ref, out, "short_queries", ref_fp64=ref64, heads=list(shape), case=case, variant=variant)
 
@@ -234,11 +233,11 @@ def test_split_counts_agree(S):
     T = d["q"].shape[0]
     os.environ["KVQ_SPLITS"] = "1"
     try:
-        one = ck.decode_attention(*args, torch.empty_like(d["q"]), *rest, max_query_len=4).cpu()
+        one = ck.decode_attention(*args, nan_like(d["q"]), *rest, max_query_len=4).cpu()
     finally:
         del os.environ["KVQ_SPLITS"]
-    segm = (torch.empty(T, 28, S, 128, device=DEV), torch.empty(T, 28, S, device=DEV), torch.empty(T, 28, S, device=DEV))
-    many = ck.decode_attention(*args, torch.empty_like(d["q"]), *rest, segm=segm, max_query_len=4).cpu()
+    segm = nan_segm(T, 28, S, 128)
+    many = ck.decode_attention(*args, nan_like(d["q"]), *rest, segm=segm, max_query_len=4).cpu()
     err = O.compare(one, many)
     record("split_vs_single", S=S, **err)
     assert err["rel_l2"] < 1e-3 and err["max_abs"] <= 1e-2
@@ -272,7 +271,7 @@ def test_mixed_batch_matches_oracle(shape, case, per_channel):
     plan = ck.plan_long(c["cu"], c["seq_lens"], 16)
     assert plan is not None and plan.has_short == (case != "prefill")
     dc = dev(c)
-    out = ck.paged_attention(dc["q"], dev(kq), dev(vq), torch.empty_like(dc["q"]), dc["cu"], dc["seq_lens"],
+    out = ck.paged_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
                              dc["block_table"], max(q_lens), c["scale"], dc["static"], plan).cpu()
     short = short_rows(c["cu"])
     res = {"long": O.compare(ref[~short], out[~short])["rel_l2"]}
@@ -293,7 +292,7 @@ def test_long_path_uses_gpu_lengths():
     bt = torch.cat([c["block_table"], c["block_table"][:, :1].expand(-1, 2)], 1)
     plan = ck.plan_long(c["cu"], c["seq_lens"] + 5, 16)
     dc = dev(c)
-    out = ck.paged_attention(dc["q"], dev(kq), dev(vq), torch.empty_like(dc["q"]), dc["cu"], dc["seq_lens"],
+    out = ck.paged_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
                              dev(bt), 300, c["scale"], dc["static"], plan).cpu()
     assert O.compare(ref, out)["rel_l2"] < 1e-2
 
@@ -308,8 +307,8 @@ def test_dequant_pages_bit_exact(per_channel, D):
     src_req, src_j = torch.from_numpy(plan.src_req), torch.from_numpy(plan.src_j)
     ko_ref, vo_ref = O.dequant_pages_ref(kq, vq, c["block_table"], src_req, src_j, c["static"])
     P = src_req.shape[0]
-    ko = torch.empty(P, 16, 4, D, dtype=torch.bfloat16, device=DEV)
-    vo = torch.empty_like(ko)
+    ko = torch.full((P, 16, 4, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vo = nan_like(ko)
     ck.ext().dequant_pages(dev(kq), dev(vq), ko, vo, dev(c["block_table"]), dev(src_req), dev(src_j),
                            dev(c["static"]["k_scale"]), dev(c["static"]["v_scale"]))
     assert torch.equal(ko.cpu().view(torch.int16), ko_ref.view(torch.int16))
@@ -326,8 +325,8 @@ def test_dequant_pages_vllm_layout():
     plan = ck.plan_long(c["cu"], c["seq_lens"], 16)
     src_req, src_j = torch.from_numpy(plan.src_req), torch.from_numpy(plan.src_j)
     ko_ref, vo_ref = O.dequant_pages_ref(kq, vq, c["block_table"], src_req, src_j, c["static"])
-    ko = torch.empty(src_req.shape[0], 16, 4, 128, dtype=torch.bfloat16, device=DEV)
-    vo = torch.empty_like(ko)
+    ko = torch.full((src_req.shape[0], 16, 4, 128), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vo = nan_like(ko)
     ck.ext().dequant_pages(kc_d, vc_d, ko, vo, dev(c["block_table"]), dev(src_req), dev(src_j),
                            dev(c["static"]["k_scale"]), dev(c["static"]["v_scale"]))
     assert torch.equal(ko.cpu().view(torch.int16), ko_ref.view(torch.int16))
@@ -340,6 +339,55 @@ def test_attention_on_vllm_interleaved_layout():
     kv = torch.cat([kq, vq], -1).transpose(1, 2).contiguous()
     kc_d, vc_d = dev(kv).transpose(1, 2).split(128, dim=-1)
     d = dev(c)
-    out = ck.decode_attention(d["q"], kc_d, vc_d, torch.empty_like(d["q"]), d["cu"], d["seq_lens"],
+    out = ck.decode_attention(d["q"], kc_d, vc_d, nan_like(d["q"]), d["cu"], d["seq_lens"],
                               d["block_table"], 128 ** -0.5, d["static"])
     check_attention(oracle_attention(c | {"scale": 128 ** -0.5}, kq, vq), out, "vllm_layout")
+
+
+# ------------------------------------------------------------------ stream-K coverage
+def _serving_batch(hq=12, hkv=2, d=128):
+    """256 requests: 188 decode rows (L 100..399) and 68 long requests the INT8 kernel skips."""
+    r = synth.rng(11)
+    ql = [int(x) for x in r.integers(39, 74, 68)] + [1] * 188
+    sl = [n + int(r.integers(0, 20)) for n in ql[:68]] + [int(x) for x in r.integers(100, 400, 188)]
+    perm = r.permutation(256)
+    return synth.paged_case(hq, hkv, [ql[i] for i in perm], [sl[i] for i in perm], head_dim=d, seed=5,
+                            dist="randn", scale=3.0)
+
+
+@pytest.fixture(scope="module")
+def serving():
+    c = _serving_batch()
+    c["static"] = synth.scales_from(c["k"].reshape(-1, 2, 128), c["v"].reshape(-1, 2, 128), True)
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    ref = oracle_attention(c, kq, vq)
+    return c, dev(kq), dev(vq), ref, short_rows(c["cu"])
+
+
+@pytest.mark.parametrize("target_waves", [0, 3, 1001, 2045])
+@pytest.mark.parametrize("splits", [1, 4, 64])
+def test_every_worker_count_covers_the_batch(serving, target_waves, splits):
+    """Every unit of the batch is computed whatever the number of persistent workgroups (here 682, 1,
+    333 and 681 workgroups of 3 wavefronts: none a multiple of the 8 XCDs) and split cap; outputs and
+    partial buffers start as NaN, so a skipped worker would show."""
+    c, kq, vq, ref, short = serving
+    d = dev(c)
+    T = d["q"].shape[0]
+    os.environ["KVQ_TARGET_WAVES"] = str(target_waves)
+    try:
+        if splits == 1:
+            os.environ["KVQ_SPLITS"] = "1"
+            try:
+                out = ck.decode_attention(d["q"], kq, vq, nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
+                                          c["scale"], d["static"], max_query_len=73)
+            finally:
+                del os.environ["KVQ_SPLITS"]
+        else:
+            out = ck.decode_attention(d["q"], kq, vq, nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
+                                      c["scale"], d["static"], segm=nan_segm(T, 12, splits, 128), max_query_len=73)
+    finally:
+        del os.environ["KVQ_TARGET_WAVES"]
+    out = out.cpu()[short]
+    assert torch.isfinite(out.float()).all(), (target_waves, splits)
+    check_attention(ref[short], out, "worker_coverage", target_waves=target_waves, splits=splits)
