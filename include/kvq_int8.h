@@ -65,12 +65,15 @@ int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, i
  * Requests with q_len == 0 or q_len > qmax are skipped (their out rows untouched).
  * Work is split stream-K: the batch is one line of units -- request by request, kv head by kv head,
  * group of up to four 16-row tiles of (token, q head) rows, then 32-key tile -- and each of about
- * target_waves / waves_per_group workgroups (0 = 8 wavefronts per compute unit) takes an equal
- * contiguous range of it. A (request, kv head, row group) that one workgroup covers whole writes out
- * directly; one that is cut writes fp32 pieces to segm_out [T, Hq, S, D] and segm_max / segm_sum
- * [T, Hq, S] (element (t, h, s) at t * seg_st + h * seg_sh + s, segm_out at that index * D + d),
- * which a second kernel merges. num_splits (<= 64) is S, the most pieces the buffers hold: no
- * segment is cut into more. num_splits == 1: nothing is cut (segm_* may be NULL). */
+ * target_waves / 4 workgroups of up to four wavefronts (target_waves 0 = 8 wavefronts per compute
+ * unit) takes an equal contiguous range of it; the wavefronts of a workgroup split a range by row
+ * tile and, for short queries, by interleaved key tiles merged in LDS. A (request, kv head, row
+ * group) that one workgroup covers whole writes out directly; one that is cut writes fp32 pieces to
+ * segm_out [T, Hq, S, D] and segm_max / segm_sum [T, Hq, S] (element (t, h, s) at
+ * t * seg_st + h * seg_sh + s, segm_out at that index * D + d), which a second kernel merges.
+ * num_splits (<= 64) is S, the most pieces the buffers hold: no segment is cut into more.
+ * num_splits == 1: nothing is cut (segm_* may be NULL). The split buffers are scratch of the call:
+ * their contents are internal (segm_sum carries the piece count in its sign), as the reference's. */
 int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
                               int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
                               int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,

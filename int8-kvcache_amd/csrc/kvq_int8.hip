@@ -293,7 +293,9 @@ struct AttnArgs {
   int num_blocks, lbs, G, qmax, ks_pc, vs_pc;
   int num_seqs, hkv;
   int max_splits;     // split buffers hold this many pieces per (token, q head); 1 = no split buffers
-  int waves;          // wavefronts per workgroup: consecutive 16-row tiles of one (request, kv head)
+  int rt;             // row tiles per workgroup: consecutive 16-row tiles of one (request, kv head)
+  int ksplit;         // key splits per workgroup: wavefront (t, k) takes every ksplit-th key tile of row tile t
+  int waves;          // rt * ksplit wavefronts per workgroup
   int workers;        // workgroups of the attention grid
   int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
   int xcd_order;      // map workgroups to workers XCD by XCD
@@ -317,7 +319,7 @@ __device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
   if (w.qlen <= 0 || w.qlen > a.qmax) return w;
   w.ntiles = max(1, (a.seq_lens[r] + TILE - 1) / TILE);
   const int rt = (w.qlen * a.G + 15) / 16;
-  w.rgroups = (rt + a.waves - 1) / a.waves;
+  w.rgroups = (rt + a.rt - 1) / a.rt;
   return w;
 }
 // Length, in work units, of each of the request's (kv head, row group) segments: its tile count, or
@@ -452,12 +454,22 @@ __device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t 
   o3 = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
 }
 
+// LDS of the key-split merge: wavefront (t, k >= 1) of a workgroup leaves its 16 rows' running max,
+// denominator and accumulators in slot (k - 1) * rt + t, lane-major ([field][lane]: conflict-free).
+constexpr int MERGE_FIELDS = 36;  // 32 accumulators (D = 128), max, denominator, 2 spare
+constexpr int MERGE_SLOTS = MAX_ROW_TILES - 1;
+constexpr int COOP_TILES = 8;     // shortest share of a key split in a split piece, in 32-key tiles
+
 // One wavefront's share of one piece of a segment: its 16-row tile (rows row0..row0+15 of the
-// (token, q head) rows of kv head kvh) over key tiles [c_begin, c_end) of request seq. The piece is
-// the segment's `part`-th of `nparts`: a whole segment writes bf16 out, a cut one an fp32 partial.
+// (token, q head) rows of kv head kvh) over the key tiles c_begin + ks, c_begin + ks + KS, ... below
+// c_end of request seq. The KS wavefronts of the row tile (ks = 0..KS-1) then merge through LDS, and
+// wavefront ks = 0 finishes the piece, the segment's `part`-th of `nparts`: a whole segment writes
+// bf16 out, a cut one an fp32 partial. Every wavefront of the workgroup calls this for every piece
+// (inactive ones -- row tiles past the request's rows -- only join the barriers of the merge).
 template <int D, int PF>
 __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
-                                               int c_begin, int c_end, int part, int nparts, int lane) {
+                                               int c_begin, int c_end, int ks, int KS, int rtile, bool active,
+                                               int part, int nparts, float* lds, int lane) {
   constexpr int KPL = D / 4;        // K bytes per lane and key
   constexpr int KSTEPS = D / 64;    // x64 MFMAs per 16-key block
   constexpr int VT = D / 16;        // PV channel tiles = V bytes per lane and key
@@ -474,10 +486,15 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   c_end = __builtin_amdgcn_readfirstlane(c_end);
   part = __builtin_amdgcn_readfirstlane(part);
   nparts = __builtin_amdgcn_readfirstlane(nparts);
+  ks = __builtin_amdgcn_readfirstlane(ks);
+  KS = __builtin_amdgcn_readfirstlane(KS);
   const int n = lane & 15, g = lane >> 4;
   const int G = a.G;
   const int L = a.seq_lens[seq];
-  if (L <= 0) c_end = c_begin;  // no keys (malformed): rows come out 0, nothing is read
+  if (L <= 0 || !active) c_end = c_begin;  // no keys (malformed) or no rows: nothing is read
+  // this wavefront's tiles: c_begin + ks + j * KS, j < nt
+  const int nt = c_begin + ks < c_end ? (c_end - c_begin - ks + KS - 1) / KS : 0;
+  auto tile = [&](int j) { return c_begin + ks + j * KS; };
   const int* bt = a.block_table + (int64_t)seq * a.bt_stride;
   const int bs = 1 << a.lbs;
 
@@ -534,9 +551,9 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   };
 
   KVTile<D> ring[PF];
-  if (c_begin < c_end) {
+  if (nt > 0) {
 #pragma unroll
-    for (int j = 0; j < PF - 1; ++j) load(ring[j], min(c_begin + j, c_end - 1));
+    for (int j = 0; j < PF - 1; ++j) load(ring[j], tile(min(j, nt - 1)));
   }
 
   // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
@@ -670,33 +687,71 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   // Loads are never skipped (past the end they re-read the last tile, an L2 hit), so every wait
   // in the loop is for exactly the oldest tile. The first PF - 1 tiles were requested before the q
   // prologue. Tiles below full_end have no masked key for any row of the wavefront; the first loop
-  // runs whole rounds of them, the second the rest (masked or not) -- both start rounds at
-  // c_begin + k * PF, so the ring slot of every tile is a compile-time index. ----
-  if (c_begin < c_end) {
-    const int c_last = c_end - 1;
-    const int full_end = max(c_begin, min(c_end, lim_lo > 0 ? lim_lo / TILE : 0));
-    int c0 = c_begin;
-    for (; c0 + PF <= full_end; c0 += PF) {
+  // runs whole rounds of them (j < j_full), the second the rest -- both start rounds at j = k * PF,
+  // so the ring slot of every tile is a compile-time index. ----
+  if (nt > 0) {
+    const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
+    const int j_full = min(nt, full_end > c_begin + ks ? (full_end - c_begin - ks + KS - 1) / KS : 0);
+    int j0 = 0;
+    for (; j0 + PF <= j_full; j0 += PF) {
 #pragma unroll
-      for (int j = 0; j < PF; ++j) {
-        load(ring[(j + PF - 1) % PF], min(c0 + j + PF - 1, c_last));
-        compute(std::false_type{}, ring[j], c0 + j);
+      for (int jj = 0; jj < PF; ++jj) {
+        load(ring[(jj + PF - 1) % PF], tile(min(j0 + jj + PF - 1, nt - 1)));
+        compute(std::false_type{}, ring[jj], tile(j0 + jj));
       }
     }
-    for (; c0 < c_end; c0 += PF) {
+    for (; j0 < nt; j0 += PF) {
 #pragma unroll
-      for (int j = 0; j < PF; ++j) {
-        const int c = c0 + j;
-        if (c >= c_end) break;
-        load(ring[(j + PF - 1) % PF], min(c + PF - 1, c_last));
-        compute(std::true_type{}, ring[j], c);
+      for (int jj = 0; jj < PF; ++jj) {
+        const int j = j0 + jj;
+        if (j >= nt) break;
+        load(ring[(jj + PF - 1) % PF], tile(min(j + PF - 1, nt - 1)));
+        compute(std::true_type{}, ring[jj], tile(j));
       }
     }
   }
 
   // ---- epilogue: lane (n, g) holds channels (D/4) g + (D/16) i + t of row n ----
   l = group4_sum(l);
-  if (rtok >= qlen) return;
+  if (KS > 1) {
+    // key-split merge (the formula of split_reduce_kernel): wavefronts k >= 1 publish (m, l, acc),
+    // wavefront 0 folds them in: M = max m_k, w_k = 2^(m_k - M), l = sum w_k l_k, acc = sum w_k acc_k
+    static_assert(VT * 4 + 2 <= MERGE_FIELDS, "merge slot too small");
+    // slot of wavefront (rtile, k >= 1): (k - 1) * rt + rtile
+    auto slot = [&](int k) { return lds + (size_t)((k - 1) * a.rt + rtile) * MERGE_FIELDS * WAVE + lane; };
+    if (ks > 0 && active) {
+      float* sl = slot(ks);
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sl[(4 * t + i) * WAVE] = acc[t][i];
+      sl[(4 * VT) * WAVE] = m;
+      sl[(4 * VT + 1) * WAVE] = l;
+    }
+    __syncthreads();
+    if (ks == 0 && active) {
+      float M = m;
+      for (int k = 1; k < KS; ++k) M = __builtin_fmaxf(M, slot(k)[(4 * VT) * WAVE]);
+      const float w0 = __builtin_amdgcn_exp2f(m - M);
+      l *= w0;
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] *= w0;
+      for (int k = 1; k < KS; ++k) {
+        const float* src = slot(k);
+        const float wk = __builtin_amdgcn_exp2f(src[(4 * VT) * WAVE] - M);
+        l = __builtin_fmaf(wk, src[(4 * VT + 1) * WAVE], l);
+#pragma unroll
+        for (int t = 0; t < VT; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(wk, src[(4 * t + i) * WAVE], acc[t][i]);
+      }
+      m = M;
+    }
+    __syncthreads();  // the slots are rewritten by the next piece
+  }
+  if (ks > 0 || !active || rtok >= qlen) return;
   constexpr int OPL = D / 4;
   const int head = kvh * G + rh;
   const int qt = tok + rtok;
@@ -706,6 +761,9 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
 #pragma unroll
     for (int t = 0; t < VT; ++t) vsc[VT * i + t] = a.vs_pc ? a.vs[kvh * D + OPL * g + VT * i + t] : a.vs[kvh];
   if (nparts == 1) {
+    // a row that is not cut tells the merge kernel so: -1 in its piece-0 denominator slot
+    if (a.max_splits > 1 && g == 0)
+      a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
     const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
     uint32_t o[OPL / 2];
 #pragma unroll
@@ -720,7 +778,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + part;
     if (g == 0) {
       a.segm_max[sidx] = m;
-      a.segm_sum[sidx] = l;
+      a.segm_sum[sidx] = part == nparts - 1 ? -2.f - l : l;  // the last piece is marked (l >= 0)
     }
     float* sp = a.segm_out + sidx * D + OPL * g;
 #pragma unroll
@@ -737,12 +795,18 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
 }
 
 // Stream-K attention: workgroup w walks units [w * chunk, (w + 1) * chunk) of the batch (make_plan),
-// segment by segment; its `waves` wavefronts take consecutive 16-row tiles of each segment and stream
-// the same K/V tiles at the same time (the second and later reads hit L1/L2).
+// segment by segment. Its rt * ks wavefronts split each piece: rt consecutive 16-row tiles (they
+// stream the same K/V tiles at the same time -- the second and later reads hit L1/L2), each over ks
+// interleaved sets of key tiles merged through LDS at the end of the piece. Decode rows (one row
+// tile) use 4 key splits, so a workgroup covers 4x the keys of one wavefront and a long request's
+// (kv head) is cut across workgroups 4x less often (c2: never). Pieces too short for every key split
+// to stream COOP_TILES tiles are not split: the key splits take them in turn, each alone.
 template <int D, int PF>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int rtile = wave % a.rt, kspl = wave / a.rt;  // row tile and key split of this wavefront
+  extern __shared__ float merge_lds[];  // (ksplit - 1) * rt slots, sized at launch (none without key splits)
   // workgroups are dispatched round-robin over the XCDs: give each XCD a contiguous range of workers
   // (so one XCD's L2 sees whole requests' block-table rows and q); KVQ_XCD_ORDER=0 turns it off.
   // XCD x holds the blocks b = x (mod 8), q + (x < rem) of them for W = 8 q + rem, and takes the
@@ -764,15 +828,25 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
   const bool whole = a.max_splits == 1;
+  int solo = 0;  // pieces run by a single wavefront so far (uniform across the workgroup)
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
     const int take = (int)min((long long)(seglen - off), end - pos);
     const long long first = seg_start / pl.chunk, last = (seg_start + seglen - 1) / pl.chunk;
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
-    const int row0 = (rg * a.waves + wave) * 16;
-    if (row0 < w.qlen * a.G)
-      attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, whole ? 0 : off, whole ? w.ntiles : off + take,
-                            (int)(worker - first), (int)(last - first + 1), lane);
+    const int row0 = (rg * a.rt + rtile) * 16;
+    const int c0 = whole ? 0 : off, c1 = whole ? w.ntiles : off + take;
+    // a piece long enough for every key split to stream COOP_TILES tiles is split across them and
+    // merged; shorter pieces go whole to one key split in turn (no barrier, no merge)
+    if (a.ksplit > 1 && c1 - c0 >= a.ksplit * COOP_TILES) {
+      attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
+                            (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
+    } else {
+      if (solo % a.ksplit == kspl)
+        attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, 0, 1, rtile, row0 < w.qlen * a.G,
+                              (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
+      ++solo;
+    }
     pos += take;
     off = 0;
     if (++seg == a.hkv * w.rgroups && pos < end) {  // on to the next request with work
@@ -790,25 +864,28 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // Merge the pieces of the cut segments (reference kvq/cuda/int8_kv.cu:465-503):
 //   o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30)
 // One wavefront per (request, q head, query token); lane s holds piece s's weight; lanes own D / 64
-// channels each. Rows of uncut segments were written by the attention kernel and are skipped.
+// channels each. The piece count is read from the denominators (the last piece's is stored as
+// -2 - l, a row that was not cut has -1 in slot 0 and was written by the attention kernel), so the
+// merge needs neither the plan nor any buffer beyond the split buffers of the call.
 template <int D>
 __global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
   const int seq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
-  const ReqWork w = req_work(a, seq);
-  if (w.ntiles == 0 || t >= w.qlen) return;
-  long long rstart;
-  const Plan pl = make_plan(a, lane, seq, &rstart);
-  const int kvh = h / a.G, row = t * a.G + h % a.G;
-  const int seg = kvh * w.rgroups + (row / 16) / a.waves;
-  const int seglen = seg_units(a, w);
-  const long long seg_start = rstart + (long long)seg * seglen;
-  const int S = (int)((seg_start + seglen - 1) / pl.chunk - seg_start / pl.chunk + 1);
-  if (S <= 1) return;
-  const int64_t base = (int64_t)(w.tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
+  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
+  if (qlen <= 0 || qlen > a.qmax || t >= qlen) return;
+  // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
+  // otherwise pieces 0..S-2 hold l >= 0 and the last piece -2 - l
+  const int64_t base = (int64_t)(tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
+  const float enc = lane < a.max_splits ? a.segm_sum[base + lane] : -1.f;
+  const unsigned long long neg = __ballot(enc < 0.f);
+  if (neg == 0ull) return;
+  const int last = __builtin_ctzll(neg);
+  if (last == 0) return;  // not cut
+  const int S = last + 1;
+  const float ls = lane < last ? enc : (lane == last ? -2.f - enc : 0.f);
   const float ms = lane < S ? a.segm_max[base + lane] : -INFINITY;
   const float M = wave_max(ms);
   const float wt = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
-  const float den = wave_sum(lane < S ? wt * a.segm_sum[base + lane] : 0.f);
+  const float den = wave_sum(wt * ls);
   const float inv = 1.f / __builtin_fmaxf(den, 1e-30f);
   constexpr int CPL = D / WAVE;
   float num[CPL];
@@ -820,7 +897,7 @@ __global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < CPL; ++e) num[e] = __builtin_fmaf(ws, p[e], num[e]);
   }
-  uint16_t* op = a.out + (int64_t)(w.tok + t) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
+  uint16_t* op = a.out + (int64_t)(tok + t) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
   if constexpr (CPL == 2) {
     *reinterpret_cast<uint32_t*>(op) = pack_bf16x2(num[0] * inv, num[1] * inv);
   } else {
@@ -1053,7 +1130,12 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   const int G = (int)(num_q_heads / num_kv_heads);
   const int64_t maxq = std::min<int64_t>(std::max<int64_t>(max_query_len, 1), qmax);
   const int64_t row_tiles = ((int64_t)G * maxq + 15) / 16;
-  const int waves = (int)std::min<int64_t>(MAX_ROW_TILES, row_tiles);
+  const int rt = (int)std::min<int64_t>(MAX_ROW_TILES, row_tiles);
+  // key splits fill the workgroup's 4 wavefronts when the rows take fewer (KVQ_KSPLIT=1: none)
+  const char* ks_env = getenv("KVQ_KSPLIT");
+  const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env))) : MAX_ROW_TILES;
+  const int ks = std::max(1, std::min(ks_max, MAX_ROW_TILES / rt));
+  const int waves = rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535) return fail("int8_decode_attention: grid too large");
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = k_cache; a.vc = v_cache; a.out = (uint16_t*)out;
@@ -1068,8 +1150,8 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX);
   a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
-  a.max_splits = (int)num_splits; a.waves = waves;
-  a.min_tiles = MIN_SPLIT_TILES;
+  a.max_splits = (int)num_splits; a.rt = rt; a.ksplit = ks; a.waves = waves;
+  a.min_tiles = MIN_SPLIT_TILES * ks;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   const int64_t tw = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
   a.workers = (int)std::max<int64_t>(1, std::min<int64_t>(tw / waves, INT32_MAX));
@@ -1079,17 +1161,18 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   g_ev_start = g_ev_stop = nullptr;
   if (ev0) (void)hipEventRecord(ev0, st);
   const dim3 block(WAVE * waves);
+  const size_t lds = (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
   const int pf = prefetch_depth();
   if (head_dim == 128) {
-    if (pf == 2) hipLaunchKernelGGL((attn_kernel<128, 2>), grid, block, 0, st, a);
-    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3>), grid, block, 0, st, a);
-    else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6>), grid, block, 0, st, a);
-    else if (pf == 8) hipLaunchKernelGGL((attn_kernel<128, 8>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((attn_kernel<128, 4>), grid, block, 0, st, a);
+    if (pf == 2) hipLaunchKernelGGL((attn_kernel<128, 2>), grid, block, lds, st, a);
+    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3>), grid, block, lds, st, a);
+    else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6>), grid, block, lds, st, a);
+    else if (pf == 8) hipLaunchKernelGGL((attn_kernel<128, 8>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((attn_kernel<128, 4>), grid, block, lds, st, a);
   } else {
-    if (pf == 2) hipLaunchKernelGGL((attn_kernel<64, 2>), grid, block, 0, st, a);
-    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((attn_kernel<64, 4>), grid, block, 0, st, a);
+    if (pf == 2) hipLaunchKernelGGL((attn_kernel<64, 2>), grid, block, lds, st, a);
+    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3>), grid, block, lds, st, a);
+    else hipLaunchKernelGGL((attn_kernel<64, 4>), grid, block, lds, st, a);
   }
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);

@@ -391,3 +391,71 @@ def test_every_worker_count_covers_the_batch(serving, target_waves, splits):
     out = out.cpu()[short]
     assert torch.isfinite(out.float()).all(), (target_waves, splits)
     check_attention(ref[short], out, "worker_coverage", target_waves=target_waves, splits=splits)
+
+
+# ------------------------------------------------------------------ concurrent streams
+def test_two_streams_merge_independently():
+    """Two streams run split attention on different batches at the same time (each with its own split
+    buffers); both results match their single-stream runs exactly: a launch keeps no state between or
+    across calls."""
+    cs = []
+    for seed in (1, 2):
+        c = synth.paged_case(28, 4, [1] * 24 + [3] * 8, [int(x) for x in synth.rng(seed).integers(200, 3000, 32)],
+                             seed=seed, params=synth.channel_params(4, 128))
+        c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+        kq, vq = int8_cache(c)
+        cs.append((dev(c), dev(kq), dev(vq)))
+
+    def run(i, out):
+        d, kq, vq = cs[i]
+        T = d["q"].shape[0]
+        return ck.decode_attention(d["q"], kq, vq, out, d["cu"], d["seq_lens"], d["block_table"], 128 ** -0.5, d["static"],
+                                   segm=nan_segm(T, 28, 16, 128), max_query_len=3)
+
+    ref = [run(i, nan_like(cs[i][0]["q"])).clone() for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [nan_like(cs[i][0]["q"]) for i in range(2)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rep in range(20):
+        for i, s in enumerate(streams):
+            with torch.cuda.stream(s):
+                run(i, outs[i])
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(outs[i], ref[i]), i
+
+
+# ------------------------------------------------------------------ key splits inside a workgroup
+@pytest.mark.parametrize("q_len", [1, 2, 3, 5])
+@pytest.mark.parametrize("segm", [False, True])
+def test_key_split_workgroups_agree(q_len, segm):
+    """Rows of one (request, kv head) split over 4 / 2 / 1 wavefronts of a workgroup (by query length:
+    7, 14, 21, 35 rows) and merged through LDS give the unsplit result (KVQ_KSPLIT=1) up to fp32
+    reassociation, and both match the oracle."""
+    lens = [4100, 33, 1, 517, 2048, 90, 1200, 16]
+    c = synth.paged_case(28, 4, [q_len] * 8, [max(L, q_len) for L in lens], seed=40 + q_len,
+                         params=synth.channel_params(4, 128))
+    c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    T = d["q"].shape[0]
+
+    def run():
+        return ck.decode_attention(d["q"], dev(kq), dev(vq), nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
+                                   c["scale"], d["static"], segm=nan_segm(T, 28, 16, 128) if segm else None,
+                                   max_query_len=q_len).cpu()
+    split = run()
+    os.environ["KVQ_KSPLIT"] = "1"
+    try:
+        plain = run()
+    finally:
+        del os.environ["KVQ_KSPLIT"]
+    e = O.compare(plain, split)
+    record("ksplit_vs_plain", q_len=q_len, segm=segm, **e)
+    assert torch.isfinite(split.float()).all() and e["rel_l2"] < 1e-3 and e["max_abs"] <= 1e-2, e
+    check_attention(oracle_attention(c, kq, vq), split, "ksplit_vs_oracle", q_len=q_len)
