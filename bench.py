@@ -145,10 +145,45 @@ def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
               "mean_abs": statistics.mean(e["mean_abs"] for e in errs),
               "rel_l2_max": max(e["rel_l2"] for e in errs), "bar": "max_abs<=2e-2, mean_abs<=2e-3"}
     parity["ok"] = parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3
-    return {"value": round(kv_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} whole c2 requests (32768 keys, 28/4/128) through the oracle's implementation B "
-                      f"(float64) + run_paged on the host, {t_total:.1f} s; KV bytes / s",
-            "us_per_request": round(t_total / n * 1e6, 1)}, parity
+    res = {"value": round(kv_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+           "sample": f"{n} whole c2 requests (32768 keys, 28/4/128) through the oracle's implementation B "
+                     f"(float64) + run_paged on the host, {t_total:.1f} s; KV bytes / s",
+           "us_per_request": round(t_total / n * 1e6, 1), "small_configs": cpu_small_configs(O, threads)}
+    torch.set_num_threads(threads)
+    return res, parity
+
+
+def cpu_small_configs(O, threads, reps=5):
+    """The oracle on the configurations the host finishes in moments: c0 (4 decode requests x {17, 300,
+    1024, 2049}, the whole attention) and c1's quantize + scatter (16384 tokens into the paged cache);
+    median wall ms of `reps` runs after one warm-up, with `threads` threads and with one."""
+    c0 = synth.c0_case()
+    st = c0["static"]
+    kq = O.quantize(c0["k"].float() - st["k_mu"], st["k_scale"])
+    vq = O.quantize(c0["v"].float(), st["v_scale"])
+    f = O.paged_static_attention(O.CFG32_Q32, st, True, 8)
+    c1 = synth.c1_inputs()
+    kc = torch.zeros(c1["num_blocks"], c1["block_size"], 4, 128, dtype=torch.int8)
+    vc = torch.zeros_like(kc)
+
+    def run_c0():
+        f(c0["q"].float(), kq, vq, c0["cu"], c0["seq_lens"], c0["block_table"], 128 ** -0.5)
+
+    def run_c1():
+        O.quant_cache_ref(c1["key"], c1["value"], kc, vc, c1["slots"], c1["static"])
+
+    out = {}
+    for name, fn in (("c0_attention", run_c0), ("c1_quant_cache", run_c1)):
+        for nt in (threads, 1):
+            torch.set_num_threads(nt)
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append((time.perf_counter() - t0) * 1e3)
+            out[f"{name}_ms_{nt}t"] = round(statistics.median(ts), 3)
+    return out
 
 
 # ------------------------------------------------------------------------------------------------ extras
