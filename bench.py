@@ -33,6 +33,7 @@ from kvq import cuda_kernels as ck  # noqa: E402
 
 with open(os.path.join(REPO, "BASELINE.json")) as _f:
     METRIC = json.load(_f)["metric"]
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_GBS = 8000.0          # MI355X HBM3E
 PEAK_INT8_OPS = 5.0e15     # dense int8 MFMA
 DEV = "cuda"
@@ -297,13 +298,28 @@ def bench_c4(reps=10):
     vo = torch.empty_like(ko)
     ms_dq = _median_event_ms(lambda i: ck.ext().dequant_pages(kc, vc, ko, vo, bt, src_req, src_j, st["k_scale"],
                                                               st["v_scale"]), reps, 1)
+    # the prefill consumer over the temporary bf16 cache: 4 x 16384 query tokens, causal
+    qp = torch.randn(sum(pre), hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    cu_p = torch.tensor([0] + [int(x) for x in torch.cumsum(torch.tensor(pre), 0)], dtype=torch.int32)
+    plan_p = ck.plan_long(cu_p, torch.tensor(pre), bs)
+    _, _, bt_p = plan_p.gpu(DEV)
+    tr, tw = plan_p.tiles(hq // hkv, DEV)
+    kt_p = torch.empty(plan_p.src_req.shape[0], bs, hkv, d, dtype=torch.bfloat16, device=DEV)
+    vt_p = torch.empty_like(kt_p)
+    ck.ext().dequant_pages(kc, vc, kt_p, vt_p, bt[96:], *plan_p.gpu(DEV)[:2], st["k_scale"], st["v_scale"])
+    op = torch.empty_like(qp)
+    cu_pd, sl_pd = cu_p.to(DEV), torch.tensor(pre, dtype=torch.int32, device=DEV)
+    ms_pf = _median_event_ms(lambda i: ck.ext().paged_prefill_attention(qp, kt_p, vt_p, op, cu_pd, sl_pd, bt_p, tr, tw,
+                                                                        d ** -0.5), max(3, reps // 2), 1, calls=3)
+    pf_flop = sum(L * (L + 1) // 2 for L in pre) * hq * d * 4
     dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
     dq_alg = P * bs * hkv * d * 2 * (1 + 2) + P * 12
     return {"decode_us": round(ms_dec * 1e3, 2), "decode_GBps": round(dec_alg / ms_dec / 1e6, 1),
             "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4),
             "dequant_us": round(ms_dq * 1e3, 2), "dequant_GBps": round(dq_alg / ms_dq / 1e6, 1),
             "dequant_frac": round(dq_alg / ms_dq / 1e6 / PEAK_GBS, 4), "dequant_pages": P,
-            "note": "bf16 prefill attention consumer not timed (torch fp32 stand-in for FlashAttention)"}
+            "prefill_ms": round(ms_pf, 3), "prefill_TFLOPs": round(pf_flop / ms_pf / 1e9, 1),
+            "prefill_frac_bf16": round(pf_flop / ms_pf / 1e9 / PEAK_BF16_TFLOPS, 4), "prefill_flop": pf_flop}
 
 
 def main():

@@ -96,6 +96,24 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
                       const int32_t* src_req, const int32_t* src_j, int64_t num_pages, const float* k_scale,
                       int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, void* stream);
 
+/* bf16 paged prefill attention over the temporary cache that kvq_dequant_pages fills: the consumer
+ * the reference delegates to vLLM's FlashAttention (kvq/cuda_kernels.py:128-130,
+ * flash_attn_varlen_func(q, kt, vt, out, cu_seqlens_q, seqused_k, ..., causal=True,
+ * block_table=plan.block_table)); no pybind counterpart. For the rows listed by the work list
+ * (tile_req[i], tile_row[i]): 64 rows (token, q head) = (r / G, r % G) of request tile_req[i] from
+ * row tile_row[i] on, every kv head; o = softmax(q k^T * softmax_scale) v over keys
+ * j <= seq_lens[req] - q_len + t (bottom-right causal), fp32 softmax and accumulation, P rounded to
+ * bf16 for the PV product. Caches: bf16 [num_blocks, block_size, H, D] views, element strides; key j
+ * of request r is slot j % block_size of page block_table[r * bt_stride + j / block_size].
+ * Rows not in the work list are not written. */
+int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k_cache, int64_t k_sb,
+                                int64_t k_sn, int64_t k_sh, const void* v_cache, int64_t v_sb, int64_t v_sn,
+                                int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                                const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                                int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
+                                const int32_t* tile_row, int64_t num_tiles, double softmax_scale, void* stream);
+
 /* Instrumentation, no counterpart in the reference: when set (non-NULL hipEvent_t handles), the next
  * kvq_int8_decode_attention call on this thread records `start` on its stream right before the
  * attention kernel and `stop` right after it (before the split merge), then forgets the pair. Lets a
@@ -105,7 +123,7 @@ int kvq_set_attention_events(void* start, void* stop);
 /* Text of the last error on this thread ("" if none). */
 const char* kvq_last_error(void);
 
-/* ABI version of this library (bumped on any signature change). */
+/* ABI version of this library (bumped on any signature change or new entry point). */
 int kvq_abi_version(void);
 
 #ifdef __cplusplus

@@ -979,6 +979,223 @@ __global__ __launch_bounds__(256) void dequant_pages_kernel(
 }
 
 // ------------------------------------------------------------------------------------------------
+// bf16 paged prefill attention for the long-query requests: the consumer of dequant_pages' temporary
+// bf16 cache, in place of the reference's vLLM FlashAttention call (kvq/cuda_kernels.py:106-131,
+// flash_attn_varlen_func(q, kt, vt, ..., causal=True, block_table=plan.block_table)).
+//   o = softmax(q k^T * scale, bottom-right causal) v   per (token, q head), fp32 softmax and
+//   accumulation, bf16 operands -- P is rounded to bf16 for the PV product, as FlashAttention does.
+// A workgroup takes 64 (token, q head) rows of one (request, kv head) (rows = token * G + head: the G
+// q heads of a kv head share every K/V tile), 4 wavefronts x 16 rows. 32-key K/V tiles are staged in
+// LDS (double buffered, one barrier per tile): K row-major, V transposed, so both MFMA operands are
+// contiguous LDS reads. Per wavefront and tile:
+//   QK  S^T[key][row]  = K . Q^T     v_mfma_f32_16x16x32_bf16, A = K (16 keys), B = q rows
+//   PV  O^T[chan][row] = V^T . P^T   v_mfma_f32_16x16x32_bf16, K = the 32-key tile
+// The QK accumulator lane (row n, group g) holds keys 16b + 4g + i -- the 8 key slots it feeds to the
+// PV B operand (slot j: key 4g + j for j < 4, 16 + 4g + j - 4 after), so P stays in its lane; the
+// V^T operand reads the same keys: two 8-byte LDS reads per channel tile.
+// ------------------------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct PrefillArgs {
+  const uint16_t* q;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  uint16_t* out;
+  const int* cu_q;
+  const int* seq_lens;
+  const int* block_table;
+  const int* tile_req;   // workgroup x: request and first row of its 64 rows
+  const int* tile_row;
+  int64_t q_st, q_sh, o_st, o_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, bt_stride;  // elements
+  float sm_log2;         // softmax_scale * log2(e)
+  int G, lbs, num_blocks;
+};
+
+constexpr int PR_ROWS = 64;                 // rows per workgroup
+constexpr int PR_KEYS = 32;                 // keys per tile
+constexpr int PR_VT = PR_KEYS + 8;          // V^T row in LDS: 32 keys + 8 of padding (80 bytes)
+
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  bf2 h;
+  h.x = (__bf16)a;
+  h.y = (__bf16)b;
+  return *reinterpret_cast<uint32_t*>(&h);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+  constexpr int DS = D / 32;                // 32-channel chunks of the QK contraction
+  constexpr int VT = D / 16;                // PV channel tiles
+  constexpr int LPK = 256 / PR_KEYS;        // loader lanes per key (8)
+  constexpr int EPL = D / LPK;              // bf16 elements per loader lane and tile (16 or 8)
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][PR_KEYS * D];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * PR_VT];
+
+  const int kvh = blockIdx.y;
+  const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int n = lane & 15, g = lane >> 4;
+  const int r = a.tile_req[blockIdx.x], row0 = a.tile_row[blockIdx.x];
+  const int tok = a.cu_q[r], Q = a.cu_q[r + 1] - tok, L = a.seq_lens[r];
+  const int G = a.G, bs = 1 << a.lbs;
+  const int* bt = a.block_table + (int64_t)r * a.bt_stride;
+
+  // this lane's row, its token and its visible keys [0, lim) (bottom-right causal)
+  const int R = row0 + wave * 16 + n, t = R / G, hq = kvh * G + R % G;
+  const bool valid = t < Q;
+  const int lim = L - Q + 1 + t;
+  // keys the workgroup needs: up to the last row's limit
+  const int t_last = min(Q - 1, (row0 + PR_ROWS - 1) / G);
+  const int kend = max(0, min(L, L - Q + 1 + t_last));
+  const int ntiles = (kend + PR_KEYS - 1) / PR_KEYS;
+  // this wavefront's rows: the smallest and largest limit among its valid ones
+  const int wt0 = (row0 + wave * 16) / G, wt1 = min(Q - 1, (row0 + wave * 16 + 15) / G);
+  const bool wave_any = wt0 < Q;
+  const int lim_lo = L - Q + 1 + wt0, lim_hi = L - Q + 1 + wt1;
+
+  // q rows as the B operand: lane (n, g) holds channels 32 s + 8 g .. + 7 of row n
+  bf16x8 qop[DS];
+  {
+    const uint16_t* qp = a.q + (int64_t)(tok + t) * a.q_st + (int64_t)hq * a.q_sh + 8 * g;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (valid) w = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+      qop[s] = *reinterpret_cast<bf16x8*>(&w);
+    }
+  }
+
+  // loader: thread th copies channels e0 .. e0 + EPL - 1 of key th / LPK of a tile
+  const int lkey = threadIdx.x / LPK, e0 = (threadIdx.x % LPK) * EPL;
+  u32x4 kreg[EPL / 8], vreg[EPL / 8];
+  auto fetch = [&](int c) {
+    const int key = c * PR_KEYS + lkey;
+    const int idx = min(key, max(kend - 1, 0)) >> a.lbs;
+    int page = bt[idx];
+    page = (page >= 0 && page < a.num_blocks) ? page : 0;
+    const int slot = min(key, max(kend - 1, 0)) & (bs - 1);
+    const uint16_t* kp = a.kc + (int64_t)page * a.k_sb + (int64_t)slot * a.k_sn + (int64_t)kvh * a.k_sh + e0;
+    const uint16_t* vp = a.vc + (int64_t)page * a.v_sb + (int64_t)slot * a.v_sn + (int64_t)kvh * a.v_sh + e0;
+#pragma unroll
+    for (int u = 0; u < EPL / 8; ++u) {
+      kreg[u] = reinterpret_cast<const u32x4*>(kp)[u];
+      vreg[u] = reinterpret_cast<const u32x4*>(vp)[u];
+    }
+  };
+  auto stage = [&](int buf) {
+    uint16_t* kd = k_lds[buf] + lkey * D + e0;
+#pragma unroll
+    for (int u = 0; u < EPL / 8; ++u) reinterpret_cast<u32x4*>(kd)[u] = kreg[u];
+    uint16_t* vd = v_lds[buf] + e0 * PR_VT + lkey;
+#pragma unroll
+    for (int u = 0; u < EPL / 8; ++u) {
+      const uint32_t w[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        vd[(8 * u + 2 * j) * PR_VT] = (uint16_t)(w[j] & 0xffffu);
+        vd[(8 * u + 2 * j + 1) * PR_VT] = (uint16_t)(w[j] >> 16);
+      }
+    }
+  };
+
+  float m = -1e30f, l = 0.f;
+  f32x4 acc[VT];
+#pragma unroll
+  for (int tt = 0; tt < VT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](auto masked_t, int buf, int c) {
+    constexpr bool MASKED = decltype(masked_t)::value;
+    const int n0 = c * PR_KEYS;
+    const uint16_t* kb = k_lds[buf];
+    f32x4 sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + (16 * b + n) * D + 32 * s + 8 * g);
+        z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s], z, 0, 0, 0);
+      }
+      sc[b] = z;
+    }
+    float sv[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = sc[b][i] * a.sm_log2;
+        if (MASKED && n0 + 16 * b + 4 * g + i >= lim) v = -INFINITY;
+        sv[b][i] = v;
+        mx = __builtin_fmaxf(mx, v);
+      }
+    mx = group4_fmax(mx);
+    const float mnew = __builtin_fmaxf(m, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    float p[2][4], psum = 0.f;
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[b][i] = __builtin_amdgcn_exp2f(sv[b][i] - mnew);
+        psum += p[b][i];
+      }
+    l = __builtin_fmaf(l, alpha, psum);
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int tt = 0; tt < VT; ++tt) acc[tt] *= alpha;
+    }
+    u32x4 pw;
+    pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
+    pw.y = pack_bf16x2_rne(p[0][2], p[0][3]);
+    pw.z = pack_bf16x2_rne(p[1][0], p[1][1]);
+    pw.w = pack_bf16x2_rne(p[1][2], p[1][3]);
+    const bf16x8 pop = *reinterpret_cast<bf16x8*>(&pw);
+    const uint16_t* vb = v_lds[buf];
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt) {
+      const uint16_t* vr = vb + (16 * tt + n) * PR_VT + 4 * g;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16);
+      u32x4 vw = {lo.x, lo.y, hi.x, hi.y};
+      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<bf16x8*>(&vw), pop, acc[tt], 0, 0, 0);
+    }
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    for (int c = 0; c < ntiles; ++c) {
+      const int buf = c & 1;
+      if (c + 1 < ntiles) fetch(c + 1);
+      const int n0 = c * PR_KEYS;
+      if (wave_any && n0 < lim_hi) {  // the wavefront has rows that see keys of this tile
+        if (n0 + PR_KEYS <= lim_lo) compute(std::false_type{}, buf, c);
+        else compute(std::true_type{}, buf, c);
+      }
+      if (c + 1 < ntiles) stage(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  l = group4_sum(l);
+  if (!valid) return;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  // lane (n, g) holds channels 16 tt + 4 g + i of row n
+  uint16_t* orow = a.out + (int64_t)(tok + t) * a.o_st + (int64_t)hq * a.o_sh + 4 * g;
+#pragma unroll
+  for (int tt = 0; tt < VT; ++tt) {
+    u32x2 w;
+    w.x = pack_bf16x2_rne(acc[tt][0] * inv, acc[tt][1] * inv);
+    w.y = pack_bf16x2_rne(acc[tt][2] * inv, acc[tt][3] * inv);
+    *reinterpret_cast<u32x2*>(orow + 16 * tt) = w;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Host side: argument checks, launches, error reporting.
 // ------------------------------------------------------------------------------------------------
 thread_local std::string g_err;
@@ -1036,13 +1253,43 @@ extern "C" {
 
 const char* kvq_last_error(void) { return g_err.c_str(); }
 
+int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k_cache, int64_t k_sb,
+                                int64_t k_sn, int64_t k_sh, const void* v_cache, int64_t v_sb, int64_t v_sn,
+                                int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                                const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                                int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
+                                const int32_t* tile_row, int64_t num_tiles, double softmax_scale, void* stream) {
+  if (head_dim != 64 && head_dim != 128) return fail("paged_prefill_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
+  if (block_size < 16 || !pow2(block_size)) return fail("paged_prefill_attention: block_size must be a power of two >= 16");
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_kv_heads > 65535)
+    return fail("paged_prefill_attention: bad head counts Hq=%lld Hkv=%lld", (long long)num_q_heads, (long long)num_kv_heads);
+  if (num_tiles < 0 || num_tiles > INT32_MAX || num_blocks > INT32_MAX) return fail("paged_prefill_attention: bad sizes");
+  if (num_tiles == 0) { g_err.clear(); return KVQ_OK; }
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_st | q_sh | o_st | o_sh) % 8 ||
+      (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 8)
+    return fail("paged_prefill_attention: rows must be 16-byte aligned (base pointers and strides)");
+  PrefillArgs a;
+  a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache; a.out = (uint16_t*)out;
+  a.cu_q = cu_seqlens_q; a.seq_lens = seq_lens; a.block_table = block_table; a.tile_req = tile_req; a.tile_row = tile_row;
+  a.q_st = q_st; a.q_sh = q_sh; a.o_st = o_st; a.o_sh = o_sh;
+  a.k_sb = k_sb; a.k_sn = k_sn; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sn = v_sn; a.v_sh = v_sh; a.bt_stride = bt_stride;
+  a.sm_log2 = (float)(softmax_scale * 1.4426950408889634);
+  a.G = (int)(num_q_heads / num_kv_heads); a.lbs = log2i(block_size); a.num_blocks = (int)num_blocks;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)num_tiles, (unsigned)num_kv_heads);
+  if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(256), 0, st, a);
+  return launched("paged_prefill_attention");
+}
+
 int kvq_set_attention_events(void* start, void* stop) {
   g_ev_start = reinterpret_cast<hipEvent_t>(start);
   g_ev_stop = reinterpret_cast<hipEvent_t>(stop);
   return KVQ_OK;
 }
 
-int kvq_abi_version(void) { return 2; }
+int kvq_abi_version(void) { return 3; }
 
 int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
                     int64_t val_sh, int8_t* k_cache, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh, int8_t* v_cache,

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -24,6 +24,9 @@ SIGNATURES = {
                                   _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr],
     "kvq_dequant_pages": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _ptr,
                           _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
+    "kvq_paged_prefill_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
+                                    _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64,
+                                    _f64, _ptr],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_last_error": [],
     "kvq_abi_version": [],

@@ -182,6 +182,28 @@ class _Ext:
                      block_table.data_ptr(), block_table.stride(0), src_req.data_ptr(), src_j.data_ptr(), n,
                      ks.data_ptr(), kcols, vs.data_ptr(), vcols, _stream(kc))
 
+    # consumer of the temporary cache: in place of flash_attn_varlen_func (kvq/cuda_kernels.py:128-130)
+    def paged_prefill_attention(self, q, kt, vt, out, cu_q, seq_lens, block_table, tile_req, tile_row, softmax_scale):
+        n = tile_req.shape[0]
+        if n == 0:
+            return
+        _check_cuda("paged_prefill_attention", q, kt, vt, out, cu_q, seq_lens, block_table, tile_req, tile_row)
+        _check(q.dtype == torch.bfloat16 and kt.dtype == torch.bfloat16 and vt.dtype == torch.bfloat16 and
+               out.dtype == torch.bfloat16, "paged_prefill_attention: q, caches and out must be bf16")
+        _check(kt.dim() == 4 and vt.shape == kt.shape and kt.stride(3) == 1 and vt.stride(3) == 1 and q.stride(2) == 1
+               and out.stride(2) == 1 and out.shape[1:] == q.shape[1:] and q.shape[2] == kt.shape[3],
+               "paged_prefill_attention: unsupported shape/layout")
+        for t, nm in ((cu_q, "cu_seqlens_q"), (seq_lens, "seq_lens"), (block_table, "block_table"),
+                      (tile_req, "tile_req"), (tile_row, "tile_row")):
+            _check(t.dtype == torch.int32, f"paged_prefill_attention: {nm} must be int32")
+        _check(block_table.stride(-1) == 1 and tile_row.shape[0] == n, "paged_prefill_attention: index layout")
+        P, bs, Hkv, d = kt.shape
+        _native.call("kvq_paged_prefill_attention", q.data_ptr(), q.stride(0), q.stride(1), kt.data_ptr(), kt.stride(0),
+                     kt.stride(1), kt.stride(2), vt.data_ptr(), vt.stride(0), vt.stride(1), vt.stride(2), P, bs, Hkv, d,
+                     out.data_ptr(), out.stride(0), out.stride(1), cu_q.data_ptr(), seq_lens.data_ptr(),
+                     block_table.data_ptr(), block_table.stride(0), q.shape[1], tile_req.data_ptr(),
+                     tile_row.data_ptr(), n, float(softmax_scale), _stream(q))
+
 
 def ext():
     """The native library (loaded once). Raises if libkvq_int8.so is missing -- callable eagerly at
@@ -256,12 +278,35 @@ class LongPlan:
     max_seqlen_k: int           # from the host-side upper bound
     has_short: bool             # any request left for the INT8 kernel
     block_size: int             # page size of both caches
+    long_req: np.ndarray = None  # [R] the long requests, their query lengths and host key-count bounds
+    long_qlen: np.ndarray = None
+    long_seq: np.ndarray = None
     _gpu: tuple = None
+    _tiles: dict = None
 
     def gpu(self, device):
         if self._gpu is None:
             self._gpu = tuple(torch.from_numpy(a).to(device) for a in (self.src_req, self.src_j, self.block_table))
         return self._gpu
+
+    def tiles(self, group, device, rows=64):
+        """Work list of the prefill kernel for `group` q heads per kv head: (request, first row) of
+        every `rows` (token, q head) rows of the long requests, the ones with the most keys to read
+        first (they finish last). Built on the host, copied once per plan and group."""
+        if self._tiles is None:
+            self._tiles = {}
+        if group not in self._tiles:
+            req, row, cost = [], [], []
+            for r, qn, sl in zip(self.long_req.tolist(), self.long_qlen.tolist(), self.long_seq.tolist()):
+                for r0 in range(0, qn * group, rows):
+                    t_last = min(qn - 1, (r0 + rows - 1) // group)
+                    req.append(r)
+                    row.append(r0)
+                    cost.append(sl - qn + 1 + t_last)
+            order = np.argsort(-np.asarray(cost, dtype=np.int64), kind="stable")
+            self._tiles[group] = tuple(torch.from_numpy(np.asarray(x, dtype=np.int32)[order]).to(device)
+                                       for x in (req, row))
+        return self._tiles[group]
 
 
 def plan_long(query_start_loc_cpu, seq_lens_cpu, block_size):
@@ -286,54 +331,26 @@ def plan_long(query_start_loc_cpu, seq_lens_cpu, block_size):
     bt = np.zeros((nreq, width), dtype=np.int32)
     bt[src_req, src_j] = np.arange(total, dtype=np.int32)
     return LongPlan(src_req=src_req, src_j=src_j, block_table=bt, max_seqlen_k=int(seq[is_long].max()),
-                    has_short=bool((q_lens[~is_long] > 0).any()), block_size=block_size)
-
-
-def _prefill_attention(q, kt, vt, out, cu_q, seq_lens, src_first, softmax_scale, rows_per_chunk=1024):
-    """bf16-cache prefill attention for the long requests (the consumer of dequant_pages; the
-    reference calls vLLM's FlashAttention here, kvq/cuda_kernels.py:128-130). Requests are read from
-    the temporary cache (their pages are consecutive there), bottom-right causal, fp32 math.
-    Needs the host copies of cu_q / seq_lens, so it runs outside graph capture (as the reference's
-    long path does)."""
-    bs, hkv, d = kt.shape[1:]
-    hq = q.shape[1]
-    g = hq // hkv
-    cu = cu_q.tolist()
-    lens = seq_lens.tolist()
-    for r, first in src_first.items():
-        n, L = cu[r + 1] - cu[r], int(lens[r])
-        npg = -(-L // bs)
-        k = kt[first:first + npg].reshape(npg * bs, hkv, d)[:L].float()          # [L, Hkv, D]
-        v = vt[first:first + npg].reshape(npg * bs, hkv, d)[:L].float()
-        kT = k.permute(1, 2, 0).contiguous()                                       # [Hkv, D, L]
-        vv = v.permute(1, 0, 2).contiguous()                                       # [Hkv, L, D]
-        for s in range(0, n, rows_per_chunk):
-            e = min(n, s + rows_per_chunk)
-            qc = q[cu[r] + s:cu[r] + e].float().reshape(e - s, hkv, g, d).permute(1, 0, 2, 3)
-            qc = qc.reshape(hkv, (e - s) * g, d).contiguous()                      # rows (t, h)
-            sc = torch.matmul(qc, kT) * softmax_scale                              # [Hkv, rows, L]
-            qpos = (L - n) + torch.arange(s, e, device=q.device)
-            mask = torch.arange(L, device=q.device)[None, :] <= qpos[:, None]       # [rows_t, L]
-            sc = sc.reshape(hkv, e - s, g, L).masked_fill(~mask[None, :, None, :], float("-inf"))
-            p = torch.softmax(sc, dim=-1).reshape(hkv, (e - s) * g, L)
-            o = torch.matmul(p, vv).reshape(hkv, e - s, g, d).permute(1, 0, 2, 3).reshape(e - s, hq, d)
-            out[cu[r] + s:cu[r] + e] = o.to(out.dtype)
+                    has_short=bool((q_lens[~is_long] > 0).any()), block_size=block_size,
+                    long_req=np.nonzero(is_long)[0].astype(np.int32), long_qlen=q_lens[is_long].astype(np.int64),
+                    long_seq=seq[is_long].astype(np.int64))
 
 
 def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, max_query_len, plan, softmax_scale,
                    static):
-    """Dequantize the long requests' pages (HIP kernel), then bf16-cache attention over them
-    (reference kvq/cuda_kernels.py:106-131). Short requests are left to decode_attention."""
+    """Dequantize the long requests' pages into a temporary bf16 paged cache (dequant_pages), then bf16
+    paged prefill attention over it (reference kvq/cuda_kernels.py:106-131, which calls vLLM's
+    FlashAttention with block_table = plan.block_table). Only the long requests' rows are written;
+    short requests are left to decode_attention. The key counts are read on the device (seq_lens), the
+    plan's host lengths only size the temporary cache and order the work."""
     bs, h, d = k_cache.shape[1:]
     _check(bs == plan.block_size, f"block size {bs} != plan block size {plan.block_size}")
-    src_req, src_j, _ = plan.gpu(q.device)
+    src_req, src_j, bt_tmp = plan.gpu(q.device)
     kt = torch.empty(src_req.shape[0], bs, h, d, dtype=q.dtype, device=q.device)
     vt = torch.empty_like(kt)
     ext().dequant_pages(k_cache, v_cache, kt, vt, block_table, src_req, src_j, static["k_scale"], static["v_scale"])
-    first = {}
-    for p, r in enumerate(plan.src_req.tolist()):
-        first.setdefault(r, p)
-    _prefill_attention(q, kt, vt, out, cu_seqlens_q.cpu(), seq_lens.cpu(), first, softmax_scale)
+    tile_req, tile_row = plan.tiles(q.shape[1] // h, q.device)
+    ext().paged_prefill_attention(q, kt, vt, out, cu_seqlens_q, seq_lens, bt_tmp, tile_req, tile_row, softmax_scale)
     return out
 
 
