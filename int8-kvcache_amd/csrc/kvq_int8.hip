@@ -986,13 +986,17 @@ __global__ __launch_bounds__(256) void dequant_pages_kernel(
 //   accumulation, bf16 operands -- P is rounded to bf16 for the PV product, as FlashAttention does.
 // A workgroup takes 64 (token, q head) rows of one (request, kv head) (rows = token * G + head: the G
 // q heads of a kv head share every K/V tile), 4 wavefronts x 16 rows. 32-key K/V tiles are staged in
-// LDS (double buffered, one barrier per tile): K row-major, V transposed, so both MFMA operands are
-// contiguous LDS reads. Per wavefront and tile:
+// LDS (double buffered, one barrier per tile), both row-major [key][channel] with padded rows: K rows
+// of D + 8 elements (a quarter-wavefront's 16 rows of 16 bytes fall in 16 distinct bank quads), V rows
+// of D + 16 (the 4 rows x 32 bytes of a transposing read in distinct banks). The V^T operand comes from
+// ds_read_b64_tr_b16: within a 16-lane group, lane 4a + b receives element b of the 8-byte chunks
+// addressed by lanes a, a + 4, a + 8, a + 12 -- pointing those lanes at 4 keys' rows gives every lane
+// 4 keys of one channel. Per wavefront and tile:
 //   QK  S^T[key][row]  = K . Q^T     v_mfma_f32_16x16x32_bf16, A = K (16 keys), B = q rows
 //   PV  O^T[chan][row] = V^T . P^T   v_mfma_f32_16x16x32_bf16, K = the 32-key tile
 // The QK accumulator lane (row n, group g) holds keys 16b + 4g + i -- the 8 key slots it feeds to the
 // PV B operand (slot j: key 4g + j for j < 4, 16 + 4g + j - 4 after), so P stays in its lane; the
-// V^T operand reads the same keys: two 8-byte LDS reads per channel tile.
+// V^T operand reads the same keys: two transposing 8-byte LDS reads per channel tile.
 // ------------------------------------------------------------------------------------------------
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -1014,7 +1018,6 @@ struct PrefillArgs {
 
 constexpr int PR_ROWS = 64;                 // rows per workgroup
 constexpr int PR_KEYS = 32;                 // keys per tile
-constexpr int PR_VT = PR_KEYS + 8;          // V^T row in LDS: 32 keys + 8 of padding (80 bytes)
 
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
@@ -1030,8 +1033,9 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   constexpr int VT = D / 16;                // PV channel tiles
   constexpr int LPK = 256 / PR_KEYS;        // loader lanes per key (8)
   constexpr int EPL = D / LPK;              // bf16 elements per loader lane and tile (16 or 8)
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][PR_KEYS * D];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * PR_VT];
+  constexpr int KST = D + 8, VST = D + 16;  // LDS row strides (elements)
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][PR_KEYS * KST];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][PR_KEYS * VST];
 
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1084,20 +1088,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     }
   };
   auto stage = [&](int buf) {
-    uint16_t* kd = k_lds[buf] + lkey * D + e0;
-#pragma unroll
-    for (int u = 0; u < EPL / 8; ++u) reinterpret_cast<u32x4*>(kd)[u] = kreg[u];
-    uint16_t* vd = v_lds[buf] + e0 * PR_VT + lkey;
+    uint16_t* kd = k_lds[buf] + lkey * KST + e0;
+    uint16_t* vd = v_lds[buf] + lkey * VST + e0;
 #pragma unroll
     for (int u = 0; u < EPL / 8; ++u) {
-      const uint32_t w[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vd[(8 * u + 2 * j) * PR_VT] = (uint16_t)(w[j] & 0xffffu);
-        vd[(8 * u + 2 * j + 1) * PR_VT] = (uint16_t)(w[j] >> 16);
-      }
+      reinterpret_cast<u32x4*>(kd)[u] = kreg[u];
+      reinterpret_cast<u32x4*>(vd)[u] = vreg[u];
     }
   };
+  // transposing-read addresses of this lane (as the supplier of row k' = n / 4, chunk a' = n % 4):
+  // keys 4 g + k' and 16 + 4 g + k', channels 4 a' .. 4 a' + 3 of each 16-channel tile
+  const int vrow0 = (4 * g + n / 4) * VST + 4 * (n % 4), vrow1 = vrow0 + 16 * VST;
 
   float m = -1e30f, l = 0.f;
   f32x4 acc[VT];
@@ -1114,7 +1115,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
-        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + (16 * b + n) * D + 32 * s + 8 * g);
+        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + (16 * b + n) * KST + 32 * s + 8 * g);
         z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s], z, 0, 0, 0);
       }
       sc[b] = z;
@@ -1153,14 +1154,17 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     pw.z = pack_bf16x2_rne(p[1][0], p[1][1]);
     pw.w = pack_bf16x2_rne(p[1][2], p[1][3]);
     const bf16x8 pop = *reinterpret_cast<bf16x8*>(&pw);
-    const uint16_t* vb = v_lds[buf];
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    uint16_t* vb = v_lds[buf];
 #pragma unroll
     for (int tt = 0; tt < VT; ++tt) {
-      const uint16_t* vr = vb + (16 * tt + n) * PR_VT + 4 * g;
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 16);
-      u32x4 vw = {lo.x, lo.y, hi.x, hi.y};
-      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<bf16x8*>(&vw), pop, acc[tt], 0, 0, 0);
+      // lane (n, g) receives V[4g + k][16 tt + n] and V[16 + 4g + k][16 tt + n], k = 0..3
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow0 + 16 * tt));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow1 + 16 * tt));
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 vw = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pop, acc[tt], 0, 0, 0);
     }
   };
 
