@@ -100,8 +100,9 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
  * the reference delegates to vLLM's FlashAttention (kvq/cuda_kernels.py:128-130,
  * flash_attn_varlen_func(q, kt, vt, out, cu_seqlens_q, seqused_k, ..., causal=True,
  * block_table=plan.block_table)); no pybind counterpart. For the rows listed by the work list
- * (tile_req[i], tile_row[i]): 64 rows (token, q head) = (r / G, r % G) of request tile_req[i] from
- * row tile_row[i] on, every kv head; o = softmax(q k^T * softmax_scale) v over keys
+ * (tile_req[i], tile_row[i]): rows_per_tile (= kvq_prefill_rows_per_tile()) rows (token, q head) =
+ * (r / G, r % G) of request tile_req[i] from row tile_row[i] on, every kv head;
+ * o = softmax(q k^T * softmax_scale) v over keys
  * j <= seq_lens[req] - q_len + t (bottom-right causal), fp32 softmax and accumulation, P rounded to
  * bf16 for the PV product. Caches: bf16 [num_blocks, block_size, H, D] views, element strides; key j
  * of request r is slot j % block_size of page block_table[r * bt_stride + j / block_size].
@@ -112,7 +113,11 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
                                 int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
                                 const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
                                 int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
-                                const int32_t* tile_row, int64_t num_tiles, double softmax_scale, void* stream);
+                                const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
+                                double softmax_scale, void* stream);
+
+/* Rows per work-list entry of kvq_paged_prefill_attention. No counterpart in the reference. */
+int kvq_prefill_rows_per_tile(void);
 
 /* Instrumentation, no counterpart in the reference: when set (non-NULL hipEvent_t handles), the next
  * kvq_int8_decode_attention call on this thread records `start` on its stream right before the

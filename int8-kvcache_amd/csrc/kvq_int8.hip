@@ -984,8 +984,9 @@ __global__ __launch_bounds__(256) void dequant_pages_kernel(
 // flash_attn_varlen_func(q, kt, vt, ..., causal=True, block_table=plan.block_table)).
 //   o = softmax(q k^T * scale, bottom-right causal) v   per (token, q head), fp32 softmax and
 //   accumulation, bf16 operands -- P is rounded to bf16 for the PV product, as FlashAttention does.
-// A workgroup takes 64 (token, q head) rows of one (request, kv head) (rows = token * G + head: the G
-// q heads of a kv head share every K/V tile), 4 wavefronts x 16 rows. 32-key K/V tiles are staged in
+// A workgroup takes 128 (token, q head) rows of one (request, kv head) (rows = token * G + head: the G
+// q heads of a kv head share every K/V tile), 4 wavefronts x 2 blocks of 16 rows; every K and V operand
+// read from LDS feeds the MFMAs of both blocks. 32-key K/V tiles are staged in
 // LDS (double buffered, one barrier per tile), both row-major [key][channel] with padded rows: K rows
 // of D + 8 elements (a quarter-wavefront's 16 rows of 16 bytes fall in 16 distinct bank quads), V rows
 // of D + 16 (the 4 rows x 32 bytes of a transposing read in distinct banks). The V^T operand comes from
@@ -1016,9 +1017,11 @@ struct PrefillArgs {
   int G, lbs, num_blocks;
 };
 
-constexpr int PR_ROWS = 64;                 // rows per workgroup
+constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
+constexpr int PR_ROWS = 4 * 16 * PR_RB;     // rows per workgroup (4 wavefronts)
 constexpr int PR_KEYS = 32;                 // keys per tile
 
+// two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   bf2 h;
@@ -1033,6 +1036,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   constexpr int VT = D / 16;                // PV channel tiles
   constexpr int LPK = 256 / PR_KEYS;        // loader lanes per key (8)
   constexpr int EPL = D / LPK;              // bf16 elements per loader lane and tile (16 or 8)
+  constexpr int RB = PR_RB;
   constexpr int KST = D + 8, VST = D + 16;  // LDS row strides (elements)
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][PR_KEYS * KST];
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][PR_KEYS * VST];
@@ -1045,28 +1049,37 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   const int G = a.G, bs = 1 << a.lbs;
   const int* bt = a.block_table + (int64_t)r * a.bt_stride;
 
-  // this lane's row, its token and its visible keys [0, lim) (bottom-right causal)
-  const int R = row0 + wave * 16 + n, t = R / G, hq = kvh * G + R % G;
-  const bool valid = t < Q;
-  const int lim = L - Q + 1 + t;
+  // this lane's rows (one per 16-row block), their tokens and visible keys [0, lim) (bottom-right causal)
+  const int wrow0 = row0 + wave * 16 * RB;
+  int t[RB], hq[RB], lim[RB];
+  bool valid[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int R = wrow0 + 16 * rb + n;
+    t[rb] = R / G;
+    hq[rb] = kvh * G + R % G;
+    valid[rb] = t[rb] < Q;
+    lim[rb] = L - Q + 1 + t[rb];
+  }
   // keys the workgroup needs: up to the last row's limit
   const int t_last = min(Q - 1, (row0 + PR_ROWS - 1) / G);
   const int kend = max(0, min(L, L - Q + 1 + t_last));
   const int ntiles = (kend + PR_KEYS - 1) / PR_KEYS;
   // this wavefront's rows: the smallest and largest limit among its valid ones
-  const int wt0 = (row0 + wave * 16) / G, wt1 = min(Q - 1, (row0 + wave * 16 + 15) / G);
+  const int wt0 = wrow0 / G, wt1 = min(Q - 1, (wrow0 + 16 * RB - 1) / G);
   const bool wave_any = wt0 < Q;
   const int lim_lo = L - Q + 1 + wt0, lim_hi = L - Q + 1 + wt1;
 
-  // q rows as the B operand: lane (n, g) holds channels 32 s + 8 g .. + 7 of row n
-  bf16x8 qop[DS];
-  {
-    const uint16_t* qp = a.q + (int64_t)(tok + t) * a.q_st + (int64_t)hq * a.q_sh + 8 * g;
+  // q rows as the B operand: lane (n, g) holds channels 32 s + 8 g .. + 7 of its row in each block
+  bf16x8 qop[RB][DS];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const uint16_t* qp = a.q + (int64_t)(tok + t[rb]) * a.q_st + (int64_t)hq[rb] * a.q_sh + 8 * g;
 #pragma unroll
     for (int s = 0; s < DS; ++s) {
       u32x4 w = {0u, 0u, 0u, 0u};
-      if (valid) w = *reinterpret_cast<const u32x4*>(qp + 32 * s);
-      qop[s] = *reinterpret_cast<bf16x8*>(&w);
+      if (valid[rb]) w = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+      qop[rb][s] = *reinterpret_cast<bf16x8*>(&w);
     }
   }
 
@@ -1074,11 +1087,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   const int lkey = threadIdx.x / LPK, e0 = (threadIdx.x % LPK) * EPL;
   u32x4 kreg[EPL / 8], vreg[EPL / 8];
   auto fetch = [&](int c) {
-    const int key = c * PR_KEYS + lkey;
-    const int idx = min(key, max(kend - 1, 0)) >> a.lbs;
-    int page = bt[idx];
+    const int key = min(c * PR_KEYS + lkey, max(kend - 1, 0));
+    int page = bt[key >> a.lbs];
     page = (page >= 0 && page < a.num_blocks) ? page : 0;
-    const int slot = min(key, max(kend - 1, 0)) & (bs - 1);
+    const int slot = key & (bs - 1);
     const uint16_t* kp = a.kc + (int64_t)page * a.k_sb + (int64_t)slot * a.k_sn + (int64_t)kvh * a.k_sh + e0;
     const uint16_t* vp = a.vc + (int64_t)page * a.v_sb + (int64_t)slot * a.v_sn + (int64_t)kvh * a.v_sh + e0;
 #pragma unroll
@@ -1100,61 +1112,76 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
   // keys 4 g + k' and 16 + 4 g + k', channels 4 a' .. 4 a' + 3 of each 16-channel tile
   const int vrow0 = (4 * g + n / 4) * VST + 4 * (n % 4), vrow1 = vrow0 + 16 * VST;
 
-  float m = -1e30f, l = 0.f;
-  f32x4 acc[VT];
+  float m[RB], l[RB];
+  f32x4 acc[RB][VT];
 #pragma unroll
-  for (int tt = 0; tt < VT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < RB; ++rb) {
+    m[rb] = -1e30f;
+    l[rb] = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt) acc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   auto compute = [&](auto masked_t, int buf, int c) {
     constexpr bool MASKED = decltype(masked_t)::value;
     const int n0 = c * PR_KEYS;
     const uint16_t* kb = k_lds[buf];
-    f32x4 sc[2];
+    // ---- QK: every K operand read once, used by every row block ----
+    f32x4 sc[RB][2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) sc[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
         const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + (16 * b + n) * KST + 32 * s + 8 * g);
-        z = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[s], z, 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[rb][s], sc[rb][b], 0, 0, 0);
       }
-      sc[b] = z;
     }
-    float sv[2][4];
-    float mx = -INFINITY;
+    // ---- online softmax per row block; P^T operands ----
+    bf16x8 pop[RB];
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int rb = 0; rb < RB; ++rb) {
+      float sv[2][4];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = sc[b][i] * a.sm_log2;
-        if (MASKED && n0 + 16 * b + 4 * g + i >= lim) v = -INFINITY;
-        sv[b][i] = v;
-        mx = __builtin_fmaxf(mx, v);
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = sc[rb][b][i] * a.sm_log2;
+          if (MASKED && n0 + 16 * b + 4 * g + i >= lim[rb]) v = -INFINITY;
+          sv[b][i] = v;
+          mx = __builtin_fmaxf(mx, v);
+        }
+      mx = group4_fmax(mx);
+      const float mnew = __builtin_fmaxf(m[rb], mx);
+      const float alpha = __builtin_amdgcn_exp2f(m[rb] - mnew);
+      m[rb] = mnew;
+      float p[2][4], psum = 0.f;
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[b][i] = __builtin_amdgcn_exp2f(sv[b][i] - mnew);
+          psum += p[b][i];
+        }
+      l[rb] = __builtin_fmaf(l[rb], alpha, psum);
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
       }
-    mx = group4_fmax(mx);
-    const float mnew = __builtin_fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    m = mnew;
-    float p[2][4], psum = 0.f;
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[b][i] = __builtin_amdgcn_exp2f(sv[b][i] - mnew);
-        psum += p[b][i];
-      }
-    l = __builtin_fmaf(l, alpha, psum);
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int tt = 0; tt < VT; ++tt) acc[tt] *= alpha;
+      u32x4 pw;
+      pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
+      pw.y = pack_bf16x2_rne(p[0][2], p[0][3]);
+      pw.z = pack_bf16x2_rne(p[1][0], p[1][1]);
+      pw.w = pack_bf16x2_rne(p[1][2], p[1][3]);
+      pop[rb] = *reinterpret_cast<bf16x8*>(&pw);
     }
-    u32x4 pw;
-    pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
-    pw.y = pack_bf16x2_rne(p[0][2], p[0][3]);
-    pw.z = pack_bf16x2_rne(p[1][0], p[1][1]);
-    pw.w = pack_bf16x2_rne(p[1][2], p[1][3]);
-    const bf16x8 pop = *reinterpret_cast<bf16x8*>(&pw);
+    // ---- PV: every V^T operand read once, used by every row block ----
     typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
     typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
     uint16_t* vb = v_lds[buf];
 #pragma unroll
@@ -1162,9 +1189,10 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       // lane (n, g) receives V[4g + k][16 tt + n] and V[16 + 4g + k][16 tt + n], k = 0..3
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow0 + 16 * tt));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow1 + 16 * tt));
-      typedef short s16x8 __attribute__((ext_vector_type(8)));
-      const s16x8 vw = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, vw), pop, acc[tt], 0, 0, 0);
+      const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        acc[rb][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[rb], acc[rb][tt], 0, 0, 0);
     }
   };
 
@@ -1185,17 +1213,20 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     }
   }
 
-  l = group4_sum(l);
-  if (!valid) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  // lane (n, g) holds channels 16 tt + 4 g + i of row n
-  uint16_t* orow = a.out + (int64_t)(tok + t) * a.o_st + (int64_t)hq * a.o_sh + 4 * g;
 #pragma unroll
-  for (int tt = 0; tt < VT; ++tt) {
-    u32x2 w;
-    w.x = pack_bf16x2_rne(acc[tt][0] * inv, acc[tt][1] * inv);
-    w.y = pack_bf16x2_rne(acc[tt][2] * inv, acc[tt][3] * inv);
-    *reinterpret_cast<u32x2*>(orow + 16 * tt) = w;
+  for (int rb = 0; rb < RB; ++rb) {
+    const float lr = group4_sum(l[rb]);
+    if (!valid[rb]) continue;
+    const float inv = lr > 0.f ? 1.f / lr : 0.f;
+    // lane (n, g) holds channels 16 tt + 4 g + i of its row
+    uint16_t* orow = a.out + (int64_t)(tok + t[rb]) * a.o_st + (int64_t)hq[rb] * a.o_sh + 4 * g;
+#pragma unroll
+    for (int tt = 0; tt < VT; ++tt) {
+      u32x2 w;
+      w.x = pack_bf16x2_rne(acc[rb][tt][0] * inv, acc[rb][tt][1] * inv);
+      w.y = pack_bf16x2_rne(acc[rb][tt][2] * inv, acc[rb][tt][3] * inv);
+      *reinterpret_cast<u32x2*>(orow + 16 * tt) = w;
+    }
   }
 }
 
@@ -1263,7 +1294,8 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
                                 int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
                                 const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
                                 int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
-                                const int32_t* tile_row, int64_t num_tiles, double softmax_scale, void* stream) {
+                                const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
+                                double softmax_scale, void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("paged_prefill_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("paged_prefill_attention: block_size must be a power of two >= 16");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_kv_heads > 65535)
@@ -1273,6 +1305,7 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_st | q_sh | o_st | o_sh) % 8 ||
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 8)
     return fail("paged_prefill_attention: rows must be 16-byte aligned (base pointers and strides)");
+  if (rows_per_tile != PR_ROWS) return fail("paged_prefill_attention: work list tiles must be %d rows", PR_ROWS);
   PrefillArgs a;
   a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache; a.out = (uint16_t*)out;
   a.cu_q = cu_seqlens_q; a.seq_lens = seq_lens; a.block_table = block_table; a.tile_req = tile_req; a.tile_row = tile_row;
@@ -1294,6 +1327,8 @@ int kvq_set_attention_events(void* start, void* stop) {
 }
 
 int kvq_abi_version(void) { return 3; }
+
+int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 
 int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
                     int64_t val_sh, int8_t* k_cache, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh, int8_t* v_cache,

@@ -26,7 +26,8 @@ SIGNATURES = {
                           _i64, _ptr, _ptr, _i64, _ptr, _i64, _ptr, _i64, _ptr],
     "kvq_paged_prefill_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64,
-                                    _f64, _ptr],
+                                    _i64, _f64, _ptr],
+    "kvq_prefill_rows_per_tile": [],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_last_error": [],
     "kvq_abi_version": [],

@@ -202,7 +202,12 @@ class _Ext:
                      kt.stride(1), kt.stride(2), vt.data_ptr(), vt.stride(0), vt.stride(1), vt.stride(2), P, bs, Hkv, d,
                      out.data_ptr(), out.stride(0), out.stride(1), cu_q.data_ptr(), seq_lens.data_ptr(),
                      block_table.data_ptr(), block_table.stride(0), q.shape[1], tile_req.data_ptr(),
-                     tile_row.data_ptr(), n, float(softmax_scale), _stream(q))
+                     tile_row.data_ptr(), n, self.prefill_rows, float(softmax_scale), _stream(q))
+
+    @property
+    def prefill_rows(self):
+        """(token, q head) rows per work-list entry of the prefill kernel."""
+        return int(_native.load().kvq_prefill_rows_per_tile())
 
 
 def ext():
@@ -289,13 +294,15 @@ class LongPlan:
             self._gpu = tuple(torch.from_numpy(a).to(device) for a in (self.src_req, self.src_j, self.block_table))
         return self._gpu
 
-    def tiles(self, group, device, rows=64):
+    def tiles(self, group, device, rows=None):
         """Work list of the prefill kernel for `group` q heads per kv head: (request, first row) of
         every `rows` (token, q head) rows of the long requests, the ones with the most keys to read
         first (they finish last). Built on the host, copied once per plan and group."""
+        if rows is None:
+            rows = ext().prefill_rows
         if self._tiles is None:
             self._tiles = {}
-        if group not in self._tiles:
+        if (group, rows) not in self._tiles:
             req, row, cost = [], [], []
             for r, qn, sl in zip(self.long_req.tolist(), self.long_qlen.tolist(), self.long_seq.tolist()):
                 for r0 in range(0, qn * group, rows):
@@ -304,9 +311,9 @@ class LongPlan:
                     row.append(r0)
                     cost.append(sl - qn + 1 + t_last)
             order = np.argsort(-np.asarray(cost, dtype=np.int64), kind="stable")
-            self._tiles[group] = tuple(torch.from_numpy(np.asarray(x, dtype=np.int32)[order]).to(device)
-                                       for x in (req, row))
-        return self._tiles[group]
+            self._tiles[(group, rows)] = tuple(torch.from_numpy(np.asarray(x, dtype=np.int32)[order]).to(device)
+                                               for x in (req, row))
+        return self._tiles[(group, rows)]
 
 
 def plan_long(query_start_loc_cpu, seq_lens_cpu, block_size):
