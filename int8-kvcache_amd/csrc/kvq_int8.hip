@@ -1020,6 +1020,9 @@ struct PrefillArgs {
 constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
 constexpr int PR_ROWS = 4 * 16 * PR_RB;     // rows per workgroup (4 wavefronts)
 constexpr int PR_KEYS = 32;                 // keys per tile
+constexpr float PR_SLACK = 8.f;             // log2 headroom of the reference maximum (general loop)
+constexpr float PR_FAST_SLACK = 64.f;       // largest excess over a row's first-tile maximum the fast pass takes
+constexpr int PR_STAGES = 4;                // LDS ring: tiles in flight + the one computed
 
 // two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
@@ -1030,26 +1033,46 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
   return *reinterpret_cast<uint32_t*>(&h);
 }
 
+// s_waitcnt that waits until at most n vector-memory operations of this wavefront are outstanding
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// workgroup barrier that orders LDS only (a plain __syncthreads would also drain every global load in
+// flight, which the LDS ring below keeps outstanding on purpose)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int D>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   constexpr int DS = D / 32;                // 32-channel chunks of the QK contraction
   constexpr int VT = D / 16;                // PV channel tiles
-  constexpr int LPK = 256 / PR_KEYS;        // loader lanes per key (8)
-  constexpr int EPL = D / LPK;              // bf16 elements per loader lane and tile (16 or 8)
   constexpr int RB = PR_RB;
-  constexpr int KST = D + 8, VST = D + 16;  // LDS row strides (elements)
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][PR_KEYS * KST];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][PR_KEYS * VST];
+  constexpr int CH = D / 8;                 // 16-byte chunks per key row
+  constexpr int ROWB = 2 * D;               // bytes per key row
+  constexpr int TILEB = PR_KEYS * ROWB;     // bytes per K (or V) tile
+  constexpr int RPI = 1024 / ROWB;          // key rows per DMA instruction (64 lanes x 16 bytes)
+  constexpr int IPW = TILEB / 1024 / 4;     // DMA instructions per wavefront per matrix and tile
+  constexpr int NS = PR_STAGES;
+  // XOR swizzles of the 16-byte chunks of a row: K by row % CH (the 16 rows of a K-operand read land
+  // in distinct bank quads), V by 2 * row % CH (the 4 rows x 2 chunks of a transposing read do)
+  auto kswz = [](int row) { return row % CH; };
+  auto vswz = [](int row) { return (2 * row) % CH; };
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS][2][TILEB];
 
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int n = lane & 15, g = lane >> 4;
   const int r = a.tile_req[blockIdx.x], row0 = a.tile_row[blockIdx.x];
   const int tok = a.cu_q[r], Q = a.cu_q[r + 1] - tok, L = a.seq_lens[r];
-  const int G = a.G, bs = 1 << a.lbs;
+  const int G = a.G;
   const int* bt = a.block_table + (int64_t)r * a.bt_stride;
 
-  // this lane's rows (one per 16-row block), their tokens and visible keys [0, lim) (bottom-right causal)
   const int wrow0 = row0 + wave * 16 * RB;
   int t[RB], hq[RB], lim[RB];
   bool valid[RB];
@@ -1061,16 +1084,12 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     valid[rb] = t[rb] < Q;
     lim[rb] = L - Q + 1 + t[rb];
   }
-  // keys the workgroup needs: up to the last row's limit
   const int t_last = min(Q - 1, (row0 + PR_ROWS - 1) / G);
   const int kend = max(0, min(L, L - Q + 1 + t_last));
   const int ntiles = (kend + PR_KEYS - 1) / PR_KEYS;
-  // this wavefront's rows: the smallest and largest limit among its valid ones
-  const int wt0 = wrow0 / G, wt1 = min(Q - 1, (wrow0 + 16 * RB - 1) / G);
-  const bool wave_any = wt0 < Q;
-  const int lim_lo = L - Q + 1 + wt0, lim_hi = L - Q + 1 + wt1;
+  const int wt0 = wrow0 / G;
+  const int lim_lo = L - Q + 1 + wt0;  // smallest limit of the wavefront's rows
 
-  // q rows as the B operand: lane (n, g) holds channels 32 s + 8 g .. + 7 of its row in each block
   bf16x8 qop[RB][DS];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -1083,34 +1102,52 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     }
   }
 
-  // loader: thread th copies channels e0 .. e0 + EPL - 1 of key th / LPK of a tile
-  const int lkey = threadIdx.x / LPK, e0 = (threadIdx.x % LPK) * EPL;
-  u32x4 kreg[EPL / 8], vreg[EPL / 8];
-  auto fetch = [&](int c) {
-    const int key = min(c * PR_KEYS + lkey, max(kend - 1, 0));
-    int page = bt[key >> a.lbs];
-    page = (page >= 0 && page < a.num_blocks) ? page : 0;
-    const int slot = key & (bs - 1);
-    const uint16_t* kp = a.kc + (int64_t)page * a.k_sb + (int64_t)slot * a.k_sn + (int64_t)kvh * a.k_sh + e0;
-    const uint16_t* vp = a.vc + (int64_t)page * a.v_sb + (int64_t)slot * a.v_sn + (int64_t)kvh * a.v_sh + e0;
+  // ---- DMA of tile c into ring stage st: wavefront w's instruction i fills key rows
+  // RPI * (IPW * w + i) .. + RPI - 1 of each matrix, lane l the physical chunk l % CH of row l / CH. The
+  // lane's part of the source address is fixed for the launch (kvh, channel chunk); the rows' pages are
+  // two scalar loads per tile (a 32-key tile spans at most two pages, block size >= 16). ----
+  const int bsm = (1 << a.lbs) - 1;
+  uint32_t kl[IPW], vl[IPW];   // byte offsets of the lane's chunk inside a key row of head kvh
+  int lrow[IPW];
 #pragma unroll
-    for (int u = 0; u < EPL / 8; ++u) {
-      kreg[u] = reinterpret_cast<const u32x4*>(kp)[u];
-      vreg[u] = reinterpret_cast<const u32x4*>(vp)[u];
+  for (int i = 0; i < IPW; ++i) {
+    lrow[i] = RPI * (IPW * wave + i) + lane / CH;
+    kl[i] = 2u * (uint32_t)(kvh * a.k_sh + 8 * ((lane % CH) ^ kswz(lrow[i])));
+    vl[i] = 2u * (uint32_t)(kvh * a.v_sh + 8 * ((lane % CH) ^ vswz(lrow[i])));
+  }
+  auto issue = [&](int c, int st) {
+    c = min(c, max(ntiles - 1, 0));  // past the end: reload the last tile into the free stage
+    const int kb0 = c * PR_KEYS, klast = max(kend - 1, 0);
+    const int i0 = kb0 >> a.lbs, i1 = min(kb0 + PR_KEYS - 1, klast) >> a.lbs;
+    int p0 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i0]);
+    int p1 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i1]);
+    p0 = (p0 >= 0 && p0 < a.num_blocks) ? p0 : 0;
+    p1 = (p1 >= 0 && p1 < a.num_blocks) ? p1 : 0;
+    const char* kp0 = (const char*)(a.kc + (int64_t)p0 * a.k_sb);
+    const char* kp1 = (const char*)(a.kc + (int64_t)p1 * a.k_sb);
+    const char* vp0 = (const char*)(a.vc + (int64_t)p0 * a.v_sb);
+    const char* vp1 = (const char*)(a.vc + (int64_t)p1 * a.v_sb);
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int key = min(kb0 + lrow[i], klast);       // rows past the last key re-read a valid one
+      const bool second = (key >> a.lbs) != i0;
+      const uint32_t slot = (uint32_t)(key & bsm);
+      const char* ks = (second ? kp1 : kp0) + (slot * 2u * (uint32_t)a.k_sn + kl[i]);
+      const char* vs = (second ? vp1 : vp0) + (slot * 2u * (uint32_t)a.v_sn + vl[i]);
+      __builtin_amdgcn_global_load_lds((const void*)ks, (__attribute__((address_space(3))) void*)(ring[st][0] + 1024 * (IPW * wave + i)), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)(ring[st][1] + 1024 * (IPW * wave + i)), 16, 0, 0);
     }
   };
-  auto stage = [&](int buf) {
-    uint16_t* kd = k_lds[buf] + lkey * KST + e0;
-    uint16_t* vd = v_lds[buf] + lkey * VST + e0;
+  // V^T transposing reads: this lane supplies the address of row vr0 = 4 g + n / 4 (keys 0..15 half) and
+  // vr0 + 16 (the other half: +16 rows = immediate offset), element chunk n % 4 of channel tile tt. With
+  // V's swizzle (chunk c of row r at c ^ (2 r % CH)) that is byte 32 (tt ^ (vr0 % 8)) + 16 (n % 4 / 2)
+  // + 8 (n % 2) of the row (D = 128; D = 64 the same with CH = 8).
+  static_assert(CH == 16 || CH == 8, "head_dim 128 or 64");
+  const int vr0 = 4 * g + n / 4;
+  uint32_t voff[VT];
 #pragma unroll
-    for (int u = 0; u < EPL / 8; ++u) {
-      reinterpret_cast<u32x4*>(kd)[u] = kreg[u];
-      reinterpret_cast<u32x4*>(vd)[u] = vreg[u];
-    }
-  };
-  // transposing-read addresses of this lane (as the supplier of row k' = n / 4, chunk a' = n % 4):
-  // keys 4 g + k' and 16 + 4 g + k', channels 4 a' .. 4 a' + 3 of each 16-channel tile
-  const int vrow0 = (4 * g + n / 4) * VST + 4 * (n % 4), vrow1 = vrow0 + 16 * VST;
+  for (int tt = 0; tt < VT; ++tt)
+    voff[tt] = vr0 * ROWB + 16 * ((2 * tt + ((n % 4) >> 1)) ^ vswz(vr0)) + 8 * (n & 1);
 
   float m[RB], l[RB];
   f32x4 acc[RB][VT];
@@ -1122,56 +1159,77 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     for (int tt = 0; tt < VT; ++tt) acc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  auto compute = [&](auto masked_t, int buf, int c) {
-    constexpr bool MASKED = decltype(masked_t)::value;
+  // ---- per tile: scores (QK) and each row's largest, masked for the keys past a row's limit ----
+  f32x4 sc[RB][2];
+  float lmax[RB], top[RB];
+  auto scores = [&](int st, int c) {
     const int n0 = c * PR_KEYS;
-    const uint16_t* kb = k_lds[buf];
-    // ---- QK: every K operand read once, used by every row block ----
-    f32x4 sc[RB][2];
+    const uint8_t* kb = ring[st][0];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) sc[rb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const int row = 16 * b + n;
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
-        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + (16 * b + n) * KST + 32 * s + 8 * g);
+        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + row * ROWB + 16 * ((4 * s + g) ^ kswz(row)));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[rb][s], sc[rb][b], 0, 0, 0);
+          sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[rb][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][b],
+                                                             0, 0, 0);
       }
     }
-    // ---- online softmax per row block; P^T operands ----
+    if (n0 + PR_KEYS > lim_lo) {  // a tile on the causal edge of some row of the wavefront
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (n0 + 16 * b + 4 * g + i >= lim[rb]) sc[rb][b][i] = -INFINITY;
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)  // this lane's largest score of the row in the tile (raw units)
+      lmax[rb] = __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(sc[rb][0][0], sc[rb][0][1]), sc[rb][0][2]),
+                                 __builtin_fmaxf(__builtin_fmaxf(sc[rb][0][3], sc[rb][1][0]), __builtin_fmaxf(
+                                     __builtin_fmaxf(sc[rb][1][1], sc[rb][1][2]), sc[rb][1][3])));
+  };
+  // the row's largest score of the tile, log2 units (the 4 lanes of a row agree)
+  auto row_top = [&]() {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) top[rb] = group4_fmax(lmax[rb]) * a.sm_log2;
+  };
+  // m is a reference maximum (log2 units) raised only when a score exceeds it by more than PR_SLACK:
+  // P = 2^(s c - m) <= 2^PR_SLACK (exact in fp32, in range for bf16), so acc / l are rescaled in a few
+  // tiles only -- out of the tile loop below, which therefore never changes acc conditionally.
+  auto needs_rescale = [&]() {
+    bool any = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) any |= top[rb] > m[rb] + PR_SLACK;
+    return __any(any);
+  };
+  auto rescale = [&]() {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float mnew = top[rb] > m[rb] + PR_SLACK ? top[rb] : m[rb];
+      const float alpha = __builtin_amdgcn_exp2f(m[rb] - mnew);
+      m[rb] = mnew;
+      l[rb] *= alpha;
+#pragma unroll
+      for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
+    }
+  };
+  auto softmax_pv = [&](int st) {
     bf16x8 pop[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      float sv[2][4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = sc[rb][b][i] * a.sm_log2;
-          if (MASKED && n0 + 16 * b + 4 * g + i >= lim[rb]) v = -INFINITY;
-          sv[b][i] = v;
-          mx = __builtin_fmaxf(mx, v);
-        }
-      mx = group4_fmax(mx);
-      const float mnew = __builtin_fmaxf(m[rb], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m[rb] - mnew);
-      m[rb] = mnew;
       float p[2][4], psum = 0.f;
 #pragma unroll
       for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[b][i] = __builtin_amdgcn_exp2f(sv[b][i] - mnew);
+          p[b][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[rb][b][i], a.sm_log2, -m[rb]));
           psum += p[b][i];
         }
-      l[rb] = __builtin_fmaf(l[rb], alpha, psum);
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
-      }
+      l[rb] += psum;
       u32x4 pw;
       pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
       pw.y = pack_bf16x2_rne(p[0][2], p[0][3]);
@@ -1179,37 +1237,86 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
       pw.w = pack_bf16x2_rne(p[1][2], p[1][3]);
       pop[rb] = *reinterpret_cast<bf16x8*>(&pw);
     }
-    // ---- PV: every V^T operand read once, used by every row block ----
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    typedef short s16x8 __attribute__((ext_vector_type(8)));
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-    uint16_t* vb = v_lds[buf];
+    // V^T operands (lane (n, g): V[4g + k][16 tt + n] and V[16 + 4g + k][16 tt + n], k = 0..3). The
+    // transposing reads are issued from inline assembly, 4 channel tiles per statement, each statement
+    // waiting for its own reads: the compiler would otherwise make them wait for every LDS DMA in
+    // flight (it cannot tell they read another ring stage), emptying the ring each tile.
+    const uint32_t vbase = (uint32_t)(uintptr_t)(ring[st][1]);
+    typedef unsigned long long u64;
 #pragma unroll
-    for (int tt = 0; tt < VT; ++tt) {
-      // lane (n, g) receives V[4g + k][16 tt + n] and V[16 + 4g + k][16 tt + n], k = 0..3
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow0 + 16 * tt));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + vrow1 + 16 * tt));
-      const bf16x8 vop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    for (int t0 = 0; t0 < VT; t0 += 4) {
+      u64 lo[4], hi[4];
+      const uint32_t a0 = vbase + voff[t0], a1 = vbase + voff[t0 + 1], a2 = vbase + voff[t0 + 2], a3 = vbase + voff[t0 + 3];
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %8\n"
+          "ds_read_b64_tr_b16 %1, %8 offset:%c12\n"
+          "ds_read_b64_tr_b16 %2, %9\n"
+          "ds_read_b64_tr_b16 %3, %9 offset:%c12\n"
+          "ds_read_b64_tr_b16 %4, %10\n"
+          "ds_read_b64_tr_b16 %5, %10 offset:%c12\n"
+          "ds_read_b64_tr_b16 %6, %11\n"
+          "ds_read_b64_tr_b16 %7, %11 offset:%c12\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]), "=&v"(lo[3]), "=&v"(hi[3])
+          : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "i"(16 * ROWB)
+          : "memory");
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-        acc[rb][tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[rb], acc[rb][tt], 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        u32x4 vw = {(uint32_t)lo[u], (uint32_t)(lo[u] >> 32), (uint32_t)hi[u], (uint32_t)(hi[u] >> 32)};
+        const bf16x8 vop = *reinterpret_cast<bf16x8*>(&vw);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          acc[rb][t0 + u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vop, pop[rb], acc[rb][t0 + u], 0, 0, 0);
+      }
     }
   };
 
   if (ntiles > 0) {
-    fetch(0);
-    stage(0);
-    __syncthreads();
-    for (int c = 0; c < ntiles; ++c) {
-      const int buf = c & 1;
-      if (c + 1 < ntiles) fetch(c + 1);
-      const int n0 = c * PR_KEYS;
-      if (wave_any && n0 < lim_hi) {  // the wavefront has rows that see keys of this tile
-        if (n0 + PR_KEYS <= lim_lo) compute(std::false_type{}, buf, c);
-        else compute(std::true_type{}, buf, c);
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j) issue(j, j);
+    auto next_tile = [&](int c) {
+      wait_vm<2 * IPW * (NS - 2)>();  // this wavefront's share of tile c has landed
+      lds_barrier();                  // everyone's share has; stage (c - 1) % NS is free again
+      issue(c + NS - 1, (c + NS - 1) % NS);
+      scores(c % NS, c);
+    };
+    // Fast pass: tile 0 sets each row's reference maximum (acc is still zero), later tiles only
+    // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
+    // exceeds the reference by 2^PR_FAST_SLACK; a row where one does is only flagged here -- acc is
+    // never changed under a condition, which keeps the accumulators in place in registers.
+    next_tile(0);
+    row_top();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
+    softmax_pv(0);
+    bool jump = false;  // per lane: one of its scores exceeded the row's reference by 2^PR_FAST_SLACK
+    for (int c = 1; c < ntiles; ++c) {
+      next_tile(c);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) jump |= lmax[rb] * a.sm_log2 > m[rb] + PR_FAST_SLACK;
+      softmax_pv(c % NS);
+    }
+    wait_vm<0>();
+    // Rare: a score far above its row's first tile somewhere in the workgroup -- redo the workgroup's
+    // tiles with a reference maximum raised (and acc / l rescaled) whenever a score exceeds it by
+    // 2^PR_SLACK.
+    if (__syncthreads_or(jump)) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        m[rb] = -1e30f;
+        l[rb] = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < VT; ++tt) acc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      if (c + 1 < ntiles) stage(buf ^ 1);
-      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < NS - 1; ++j) issue(j, j);
+      for (int c = 0; c < ntiles; ++c) {
+        next_tile(c);
+        row_top();
+        if (needs_rescale()) rescale();
+        softmax_pv(c % NS);
+      }
+      wait_vm<0>();  // the reloads past the end, before the wavefront exits
     }
   }
 
@@ -1218,7 +1325,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillArgs a) {
     const float lr = group4_sum(l[rb]);
     if (!valid[rb]) continue;
     const float inv = lr > 0.f ? 1.f / lr : 0.f;
-    // lane (n, g) holds channels 16 tt + 4 g + i of its row
     uint16_t* orow = a.out + (int64_t)(tok + t[rb]) * a.o_st + (int64_t)hq[rb] * a.o_sh + 4 * g;
 #pragma unroll
     for (int tt = 0; tt < VT; ++tt) {

@@ -123,3 +123,31 @@ def test_c4_prefill_full_size_sampled():
                 worst[key] = max(worst[key], e[key])
     record("c4_prefill_sampled", **worst)
     assert worst["max_abs"] <= 2e-2 and worst["rel_l2"] < 1e-2, worst
+
+
+def test_prefill_score_jump_takes_the_rescaling_pass():
+    """A key far past the first tile whose scores exceed every earlier one by much more than 2^64
+    (log2 units): the fast pass flags its workgroups and they are recomputed with rescaling; the
+    result still matches fp32 attention (where the outlier key dominates every row that sees it)."""
+    hq, hkv, d = 28, 4, 128
+    q_lens, seq_lens = [200, 40], [1000, 300]
+    cu, plan, kt, vt = _temp_cache(q_lens, seq_lens, hkv, d, 16, seed=3)
+    T = int(cu[-1])
+    q = (torch.randn(T, hq, d, generator=torch.Generator().manual_seed(4)) + 0.5).to(torch.bfloat16)
+    first = {}
+    for p, r in enumerate(plan.src_req.tolist()):
+        first.setdefault(r, p)
+    for r, key in ((0, 850), (1, 130)):                   # outliers past tile 0, visible to later rows
+        kt[first[r] + key // 16, key % 16] = 60.0
+    scale = d ** -0.5
+    out = nan_like(q.to(DEV))
+    tile_req, tile_row = plan.tiles(hq // hkv, DEV)
+    _, _, bt = plan.gpu(DEV)
+    ck.ext().paged_prefill_attention(q.to(DEV), kt.to(DEV), vt.to(DEV), out, cu.to(DEV),
+                                     torch.tensor(seq_lens, dtype=torch.int32, device=DEV), bt, tile_req, tile_row, scale)
+    out = out.cpu()
+    ref = _reference(q, kt, vt, cu, seq_lens, plan, scale)
+    got = torch.stack([out[int(cu[r]) + t] for (r, t) in ref]).float()
+    err = O.compare(torch.stack(list(ref.values())), got)
+    record("prefill_score_jump", **err)
+    assert torch.isfinite(got).all() and err["max_abs"] <= 2e-2 and err["rel_l2"] < 1e-2, err
