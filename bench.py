@@ -331,6 +331,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 5 times (HBM counter calibration)")
+    ap.add_argument("--extras", default="",
+                    help="only run these extra workloads (comma list of c1, c3, c4) and print their JSON; for "
+                         "profiling one kernel's workload")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (every kernel shards per request / "
@@ -347,6 +350,14 @@ def main():
         print(json.dumps({"copy_calibration_bytes": 1 << 30, "copies": 5}))
         return
     ck.ext()
+    if args.extras:
+        runs = {"c1": ("c1_quant_cache", bench_c1), "c3": ("c3_verify_8tok", bench_c3), "c4": ("c4_llama3_mixed", bench_c4)}
+        names = [x.strip() for x in args.extras.split(",") if x.strip()]
+        bad = [x for x in names if x not in runs]
+        if bad:
+            ap.error("unknown extras %s (choose from c1, c3, c4)" % bad)
+        print(json.dumps({"extra": {runs[x][0]: runs[x][1]() for x in names}}), flush=True)
+        return
     print("# building c2 workload", file=sys.stderr, flush=True)
     w = build_c2()
     torch.cuda.synchronize()

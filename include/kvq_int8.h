@@ -40,7 +40,11 @@ enum {
  *   kc[slot / bs, slot % bs, h, d] = sat127(rint(fl((f32(key[t,h,d]) - k_mu[h,d]) / k_scale)))
  *   vc[...]                        = sat127(rint(fl(f32(value[t,h,d]) / v_scale)))
  * for t < n_tokens whose slot is in [0, num_blocks * block_size); other slots are skipped.
- * k_scale_cols / v_scale_cols: D (per channel) or 1 (per head). */
+ * k_scale_cols / v_scale_cols: D (per channel) or 1 (per head). head_dim 64 or 128; rows, strides
+ * and the per-channel tables / k_mu 16-byte aligned. Any head count when num_heads * head_dim is a
+ * multiple of 512 and the key / value extents and a cache row's head span are below 2 GiB (the
+ * wavefront-per-token kernel); otherwise num_heads * head_dim <= 2048. Stream-ordered, allocates
+ * nothing. */
 int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
                     int64_t val_sh, int8_t* k_cache, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh, int8_t* v_cache,
                     int64_t vc_sb, int64_t vc_sn, int64_t vc_sh, const int64_t* slot_mapping, int64_t n_tokens,

@@ -25,6 +25,7 @@
 
 #include <stdint.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -130,11 +131,13 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // ------------------------------------------------------------------------------------------------
 // Fused quantize + reshape_and_cache (reference kvq/cuda/int8_kv.cu:55-84).
-// A wavefront covers whole tokens: each lane owns 8 channels of one head for the whole launch (their
-// scales, reciprocals and K means stay in registers), so a token's K and V rows are read as 1 KB
-// contiguous runs (H = 4, D = 128) and each (token, head) writes its 128-byte K and V code rows with
-// 16 consecutive lanes -- the 256-byte K|V run of a slot in vLLM's interleaved layout. Each lane walks
-// its tokens with a ring of QC_PF tokens of loads in flight.
+// Each lane owns 8 channels of one head for the whole launch (their reciprocal scales and K means in
+// registers), so a token's K and V rows are read as contiguous runs (1 KB each for H = 4, D = 128) and
+// each (token, head) writes its 128-byte K and V code rows with 16 consecutive lanes -- the 256-byte
+// K|V run of a slot in vLLM's interleaved layout. Two kernels: quant_cache_rows_kernel when a token's
+// H * D channels fill whole wavefronts (wave-uniform addressing, below), quant_cache_kernel otherwise
+// (lanes of a wavefront may hold different tokens). Both walk their tokens with a ring of loads in
+// flight.
 //
 // Codes: q0 = fl(x * r) with r = v_rcp_f32(s) (<= 1 ulp) is within 2^-22 * |q0| (<= 3.1e-5 for
 // |q0| <= 127.5) of fl(x / s). c = clamp(q0, +-127); t = fl(c + 1.5 * 2^23) holds rint(c) in its low mantissa bits,
@@ -144,9 +147,30 @@ __device__ __forceinline__ float wave_sum(float x) {
 // exact: rint(clamp(q, +-127)) = clamp(rint(q), +-127), and |q0| > 127 saturates either way.
 // ------------------------------------------------------------------------------------------------
 constexpr int QC_CPL = 8;     // channels per lane
-constexpr int QC_PF = 5;      // ring of token loads per lane (QC_PF - 1 in flight ahead)
+#ifndef QC_PF
+#define QC_PF 5               // quant_cache_kernel: ring of token loads per lane (QC_PF - 1 ahead)
+#endif
 constexpr int QC_BLOCK = 256;
+#ifndef QC_WAVES
+#define QC_WAVES 4            // at least this many waves per SIMD (<= 128 VGPRs; the row kernel fits 5)
+#endif
 constexpr float QC_MAGIC = 12582912.0f;  // 1.5 * 2^23
+#ifndef QC_NT_LOAD
+#define QC_NT_LOAD 1          // K/V rows are read once: streaming loads
+#endif
+#ifndef QC_NT_STORE
+#define QC_NT_STORE 1         // codes are written once: streaming stores
+#endif
+template <typename T>
+__device__ __forceinline__ T qc_load(const T* p) {
+  if constexpr (QC_NT_LOAD) return __builtin_nontemporal_load(p);
+  else return *p;
+}
+template <typename T>
+__device__ __forceinline__ void qc_store(T v, T* p) {
+  if constexpr (QC_NT_STORE) __builtin_nontemporal_store(v, p);
+  else *p = v;
+}
 
 // code bytes (little endian) of 4 values t = fl(c + QC_MAGIC)
 __device__ __forceinline__ uint32_t pack_magic4(float t0, float t1, float t2, float t3) {
@@ -155,9 +179,23 @@ __device__ __forceinline__ uint32_t pack_magic4(float t0, float t1, float t2, fl
   return lo | hi;
 }
 
-template <bool SUB_MU>
-__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const float (&sc)[QC_CPL],
-                                        const float (&mu)[QC_CPL]) {
+// the lane's 8 scales: 8 consecutive entries of a per-channel table (16-byte aligned), or the head's
+// one scale broadcast (pc is uniform: a scalar branch)
+__device__ __forceinline__ void load_scales8(const float* __restrict__ p, int pc, float (&o)[QC_CPL]) {
+  if (pc) {
+    const float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  } else {
+    const float v = *p;
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) o[e] = v;
+  }
+}
+
+// r: reciprocals of the lane's 8 scales; get_sc(sc) fetches the scales themselves, for the rare exact
+// pass only (so that they hold no registers)
+template <bool SUB_MU, typename GetScales>
+__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], GetScales get_sc, const float (&mu)[QC_CPL]) {
   float x[QC_CPL], t[QC_CPL];
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -178,6 +216,8 @@ __device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const
     worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
   }
   if (worst >= 0.5f - 0x1p-14f) {  // rare: a quotient near a half-integer -- redo this lane exactly
+    float sc[QC_CPL];
+    get_sc(sc);
 #pragma unroll
     for (int e = 0; e < QC_CPL; ++e) t[e] = code_exact(x[e], sc[e]) + QC_MAGIC;
   }
@@ -185,7 +225,7 @@ __device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], const
 }
 
 template <int D>
-__global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
+__global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAVES))) void quant_cache_kernel(
     const uint16_t* __restrict__ key, int64_t key_st, int64_t key_sh, const uint16_t* __restrict__ value,
     int64_t val_st, int64_t val_sh, int8_t* __restrict__ kc, int64_t kc_sb, int64_t kc_sn, int64_t kc_sh,
     int8_t* __restrict__ vc, int64_t vc_sb, int64_t vc_sn, int64_t vc_sh, const int64_t* __restrict__ slots,
@@ -207,23 +247,47 @@ __global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
   auto fetch = [&](int j, int k) {  // k clamped: past the end it re-reads the lane's last token
     const int t = t_first + min(k, steps - 1) * stride;
     slot[j] = slots[t];
-    kin[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0));
-    vin[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0));
+    kin[j] = qc_load(reinterpret_cast<const u32x4*>(key + t * key_st + h * key_sh + d0));
+    vin[j] = qc_load(reinterpret_cast<const u32x4*>(value + t * val_st + h * val_sh + d0));
   };
   // scales first, then the first tokens' rows: all in flight before anything waits
-  float kS[QC_CPL], vS[QC_CPL], kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
+  const float* kp = ks + (ks_pc ? h * D + d0 : h);
+  const float* vp = vs + (vs_pc ? h * D + d0 : h);
+  float kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
+  load_scales8(kp, ks_pc, kr);
+  load_scales8(vp, vs_pc, vr);
+  load_scales8(kmu + h * D + d0, 1, mu);
+  auto emit = [&](int j) {
+    const int64_t sl = slot[j];
+    if (sl < 0 || sl >= num_slots) return;   // padding (or out of range): skipped
+    const int64_t blk = sl >> lbs, off = sl & bmask;
+    qc_store(quant8<true>(kin[j], kr, [&](float (&sc)[QC_CPL]) { load_scales8(kp, ks_pc, sc); }, mu),
+                                reinterpret_cast<u32x2*>(kc + blk * kc_sb + off * kc_sn + h * kc_sh + d0));
+    qc_store(quant8<false>(vin[j], vr, [&](float (&sc)[QC_CPL]) { load_scales8(vp, vs_pc, sc); }, mu),
+                                reinterpret_cast<u32x2*>(vc + blk * vc_sb + off * vc_sn + h * vc_sh + d0));
+  };
+  if (steps <= QC_PF - 1) {
+    // all of the lane's tokens fit in flight at once (a step's worth of new tokens): load exactly
+    // those, then write them -- no ring, no re-reads
 #pragma unroll
-  for (int e = 0; e < QC_CPL; ++e) {
-    kS[e] = ks[ks_pc ? h * D + d0 + e : h];
-    vS[e] = vs[vs_pc ? h * D + d0 + e : h];
-    mu[e] = kmu[h * D + d0 + e];
+    for (int j = 0; j < QC_PF - 1; ++j)
+      if (j < steps) fetch(j, j);
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) {
+      kr[e] = __builtin_amdgcn_rcpf(kr[e]);
+      vr[e] = __builtin_amdgcn_rcpf(vr[e]);
+    }
+#pragma unroll
+    for (int j = 0; j < QC_PF - 1; ++j)
+      if (j < steps) emit(j);
+    return;
   }
 #pragma unroll
   for (int j = 0; j < QC_PF - 1; ++j) fetch(j, j);
 #pragma unroll
   for (int e = 0; e < QC_CPL; ++e) {
-    kr[e] = __builtin_amdgcn_rcpf(kS[e]);
-    vr[e] = __builtin_amdgcn_rcpf(vS[e]);
+    kr[e] = __builtin_amdgcn_rcpf(kr[e]);
+    vr[e] = __builtin_amdgcn_rcpf(vr[e]);
   }
   for (int k0 = 0; k0 < steps; k0 += QC_PF) {
 #pragma unroll
@@ -231,13 +295,132 @@ __global__ __launch_bounds__(QC_BLOCK) void quant_cache_kernel(
       const int k = k0 + j;
       if (k >= steps) break;
       fetch((j + QC_PF - 1) % QC_PF, k + QC_PF - 1);
-      const int64_t sl = slot[j];
-      if (sl < 0 || sl >= num_slots) continue;   // padding (or out of range): skipped
-      const int64_t blk = sl >> lbs, off = sl & bmask;
-      __builtin_nontemporal_store(quant8<true>(kin[j], kr, kS, mu),
-                                  reinterpret_cast<u32x2*>(kc + blk * kc_sb + off * kc_sn + h * kc_sh + d0));
-      __builtin_nontemporal_store(quant8<false>(vin[j], vr, vS, mu),
-                                  reinterpret_cast<u32x2*>(vc + blk * vc_sb + off * vc_sn + h * vc_sh + d0));
+      emit(j);
+    }
+  }
+}
+
+// Wavefront-row variant, for shapes where a token's H * D channels are a whole number of wavefronts
+// (H * D % 512 == 0: 8 channels per lane). Each wavefront owns 512 / D heads of a token, so the
+// token, its slot and every row base are wave-uniform: the slot is a scalar load, the K/V rows are
+// buffer loads (one descriptor per input, the token's byte offset as the scalar offset) and each
+// cache row is a buffer store through a descriptor built in scalar registers from the block address
+// -- no per-token vector address arithmetic. Same arithmetic per channel (quant8), same codes.
+//
+// The vector-memory counter (vmcnt) counts loads and stores in issue order, and a wait can only be
+// as precise as the compiler's static count of what was issued: so nothing here issues a vector
+// memory operation under a branch. A padded slot (or a ring entry past the wavefront's last token)
+// still stores, through a descriptor with no records, which the hardware's range check drops; the
+// exact pass reads its scales from LDS. The ring's waits then leave QC_ROW_PF - 1 tokens' loads and
+// the stores of earlier tokens in flight instead of draining them per token.
+#ifndef QC_ROW_PF
+#define QC_ROW_PF 5           // ring of token loads per wavefront (QC_ROW_PF - 1 in flight ahead)
+#endif
+constexpr int QC_RSRC_WORD3 = 0x00020000;          // raw buffer, 32-bit dwords (gfx9 family)
+constexpr int QC_LOAD_AUX = QC_NT_LOAD ? 2 : 0;    // 2: nontemporal
+constexpr int QC_STORE_AUX = QC_NT_STORE ? 2 : 0;
+
+template <int D>
+__global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAVES))) void quant_cache_rows_kernel(
+    const uint16_t* __restrict__ key, int key_st, int key_sh, int key_bytes, const uint16_t* __restrict__ value,
+    int val_st, int val_sh, int val_bytes, int8_t* __restrict__ kc, int64_t kc_sb, int64_t kc_sn, int kc_sh,
+    int8_t* __restrict__ vc, int64_t vc_sb, int64_t vc_sn, int vc_sh, int row_bytes, const int64_t* __restrict__ slots,
+    int n, int wpt, int64_t num_slots, int lbs, const float* __restrict__ ks, int ks_pc,
+    const float* __restrict__ vs, int vs_pc, const float* __restrict__ kmu) {
+  constexpr int LPH = D / QC_CPL;                 // lanes per head
+  constexpr int HPW = WAVE / LPH;                 // heads per wavefront
+  constexpr int CH = WAVE * QC_CPL;               // channels per wavefront
+  constexpr int WPB = QC_BLOCK / WAVE;
+  // a workgroup owns one part (HPW heads) of WPB tokens at a time; the grid is a multiple of wpt
+  const int part = blockIdx.x % wpt;
+  const int lane = threadIdx.x % WAVE;
+  const int t_first = __builtin_amdgcn_readfirstlane((blockIdx.x / wpt) * WPB + threadIdx.x / WAVE);
+  const int stride = (gridDim.x / wpt) * WPB;
+  const int h = part * HPW + lane / LPH, d0 = (lane % LPH) * QC_CPL;
+
+  // the part's scales and k_mu, loaded once per workgroup: every wavefront of the grid reads the
+  // same few lines of these tables, so per-wavefront loads would pile onto a few L2 channels
+  __shared__ float4 tab[3][CH / 4];               // k_scale, v_scale, k_mu of channels part * CH + c
+  for (int i = threadIdx.x; i < 3 * CH / 4; i += QC_BLOCK) {
+    const int t = i / (CH / 4), c = (i % (CH / 4)) * 4, ch = part * CH + c;
+    float4 v;
+    if (t == 2) v = *reinterpret_cast<const float4*>(kmu + ch);
+    else {
+      const float* tb = t == 0 ? ks : vs;
+      if (t == 0 ? ks_pc : vs_pc) v = *reinterpret_cast<const float4*>(tb + ch);
+      else { const float x = tb[ch / D]; v = float4{x, x, x, x}; }   // 4 channels never straddle a head
+    }
+    tab[t][i % (CH / 4)] = v;
+  }
+  __syncthreads();
+  if (t_first >= n) return;
+  const int steps = (n - 1 - t_first) / stride + 1;   // tokens of this wavefront: t_first + k * stride
+  const int64_t bmask = (int64_t(1) << lbs) - 1;
+  // per-lane byte offsets within a token's rows (all extents < 2^31 bytes: host)
+  const int koff = 2 * (h * key_sh + d0), voff = 2 * (h * val_sh + d0);
+  const int kcoff = h * kc_sh + d0, vcoff = h * vc_sh + d0;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)key, 0, key_bytes, QC_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)value, 0, val_bytes, QC_RSRC_WORD3);
+  int64_t slot[QC_ROW_PF];
+  u32x4 kin[QC_ROW_PF], vin[QC_ROW_PF];
+  // fetches are issued in ring order (scheduling barriers: the waits count on that order)
+  auto fetch = [&](int j, int k) {  // k clamped: past the end it re-reads the wavefront's last token
+    const int t = t_first + min(k, steps - 1) * stride;
+    slot[j] = slots[t];
+    __builtin_amdgcn_sched_barrier(0);
+    kin[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, 2 * t * key_st, QC_LOAD_AUX);
+    vin[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 2 * t * val_st, QC_LOAD_AUX);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int c4 = lane * (QC_CPL / 4);             // this lane's 8 channels: tab[.][c4], tab[.][c4 + 1]
+  auto tab8 = [&](int t, float (&o)[QC_CPL]) {
+    const float4 a = tab[t][c4], b = tab[t][c4 + 1];
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  };
+  float kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
+  auto emit = [&](int j, bool real) {
+    const int64_t sl = slot[j];
+    const bool ok = real && sl >= 0 && sl < num_slots;   // uniform; otherwise the stores are dropped
+    const int64_t blk = ok ? sl >> lbs : 0, off = ok ? sl & bmask : 0;
+    const int nrec = ok ? row_bytes : 0;
+    const __amdgpu_buffer_rsrc_t wk =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kc + blk * kc_sb + off * kc_sn), 0, nrec, QC_RSRC_WORD3);
+    const __amdgpu_buffer_rsrc_t wv =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vc + blk * vc_sb + off * vc_sn), 0, nrec, QC_RSRC_WORD3);
+    __builtin_amdgcn_raw_buffer_store_b64(quant8<true>(kin[j], kr, [&](float (&sc)[QC_CPL]) { tab8(0, sc); }, mu),
+                                          wk, kcoff, 0, QC_STORE_AUX);
+    __builtin_amdgcn_raw_buffer_store_b64(quant8<false>(vin[j], vr, [&](float (&sc)[QC_CPL]) { tab8(1, sc); }, mu),
+                                          wv, vcoff, 0, QC_STORE_AUX);
+  };
+  auto prepare = [&] {
+    tab8(0, kr);
+    tab8(1, vr);
+    tab8(2, mu);
+#pragma unroll
+    for (int e = 0; e < QC_CPL; ++e) {
+      kr[e] = __builtin_amdgcn_rcpf(kr[e]);
+      vr[e] = __builtin_amdgcn_rcpf(vr[e]);
+    }
+  };
+  if (steps <= QC_ROW_PF - 1) {
+    // all of the wavefront's tokens in flight at once (entries past the last re-read it, and drop
+    // their stores)
+#pragma unroll
+    for (int j = 0; j < QC_ROW_PF - 1; ++j) fetch(j, j);
+    prepare();
+#pragma unroll
+    for (int j = 0; j < QC_ROW_PF - 1; ++j) emit(j, j < steps);
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < QC_ROW_PF - 1; ++j) fetch(j, j);
+  prepare();
+  for (int k0 = 0; k0 < steps; k0 += QC_ROW_PF) {
+#pragma unroll
+    for (int j = 0; j < QC_ROW_PF; ++j) {
+      const int k = k0 + j;
+      fetch((j + QC_ROW_PF - 1) % QC_ROW_PF, k + QC_ROW_PF - 1);
+      emit(j, k < steps);
     }
   }
 }
@@ -1387,6 +1570,19 @@ int device_cus() {
   return cus;
 }
 
+// workgroups of QC_BLOCK threads of kernel K resident per CU at once (KVQ_QC_WG_PER_CU overrides)
+template <auto K>
+int resident_blocks() {
+  static const int nb = [] {
+    int v = 0;
+    if (const char* e = getenv("KVQ_QC_WG_PER_CU")) v = atoi(e);
+    if (v <= 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, QC_BLOCK, 0) != hipSuccess || v <= 0)) v = QC_WAVES;
+    return v;
+  }();
+  return nb;
+}
+
+
 
 }  // namespace
 
@@ -1446,29 +1642,61 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
   if (n_tokens < 0 || num_heads <= 0) return fail("quant_cache: bad sizes n=%lld H=%lld", (long long)n_tokens, (long long)num_heads);
   if (n_tokens == 0) { g_err.clear(); return KVQ_OK; }
   if (!pow2(block_size)) return fail("quant_cache: block_size must be a power of two, got %lld", (long long)block_size);
-  if (num_heads * (head_dim / QC_CPL) > QC_BLOCK) return fail("quant_cache: at most %d heads of dim %lld", (int)(QC_BLOCK * QC_CPL / head_dim), (long long)head_dim);
   if ((k_scale_cols != 1 && k_scale_cols != head_dim) || (v_scale_cols != 1 && v_scale_cols != head_dim))
     return fail("quant_cache: scale columns must be 1 or head_dim");
   if (!key || !value || !k_cache || !v_cache || !slot_mapping || !k_scale || !v_scale || !k_mu) return fail("quant_cache: null pointer");
+  if ((k_scale_cols > 1 && !aligned16(k_scale)) || (v_scale_cols > 1 && !aligned16(v_scale)) || !aligned16(k_mu))
+    return fail("quant_cache: per-channel scale tables and k_mu must be 16-byte aligned");
   if (!aligned16(key) || !aligned16(value) || !aligned16(k_cache) || !aligned16(v_cache) || (key_st | key_sh | val_st | val_sh) % 8 ||
       (kc_sb | kc_sn | kc_sh | vc_sb | vc_sn | vc_sh) % 16)
     return fail("quant_cache: rows must be 16-byte aligned (base pointers and strides)");
   if (n_tokens > INT32_MAX) return fail("quant_cache: too many tokens");
   const int H = (int)num_heads;
-  const int ipt = H * (int)(head_dim / QC_CPL), tpb = QC_BLOCK / ipt;
-  const int64_t want = (n_tokens + tpb - 1) / tpb;
-  const int grid = (int)std::min<int64_t>(want, (int64_t)device_cus() * 4);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int lbs = log2i(block_size);
   const int64_t num_slots = num_blocks * block_size;
-  auto go = [&](auto kern) {
+  const int ks_pc = k_scale_cols > 1, vs_pc = v_scale_cols > 1;
+  // byte extents the wavefront-row kernel addresses with 32-bit offsets
+  const int64_t key_bytes = 2 * ((n_tokens - 1) * key_st + (num_heads - 1) * key_sh + head_dim);
+  const int64_t val_bytes = 2 * ((n_tokens - 1) * val_st + (num_heads - 1) * val_sh + head_dim);
+  const int64_t row_bytes = (num_heads - 1) * std::max(kc_sh, vc_sh) + head_dim;
+  if ((num_heads * head_dim) % (WAVE * QC_CPL) == 0 && std::max({key_bytes, val_bytes, row_bytes}) <= INT32_MAX) {
+    // whole wavefronts per token: the wavefront-row kernel; the grid holds a whole number of tokens'
+    // wavefronts (wpt) and no more workgroups than are resident at once
+    // a workgroup owns one of the token's wpt parts for QC_BLOCK / WAVE tokens at a time (the grid
+    // is a multiple of wpt). Balanced: the fewest tokens per wavefront one resident round allows,
+    // then just enough workgroups for n at that count -- a wavefront with fewer tokens than its
+    // ring holds still issues (and drops) the rest
+    const int wpt = (int)(num_heads * head_dim / (WAVE * QC_CPL));
+    const int wpb = QC_BLOCK / WAVE;
+    auto go = [&](auto kern, int resident) {
+      const int64_t conc = std::max<int64_t>(1, (int64_t)device_cus() * resident / wpt) * wpb;  // tokens in flight
+      const int64_t per = (n_tokens + conc - 1) / conc;                                        // tokens per wavefront
+      const int64_t grid = (n_tokens + wpb * per - 1) / (wpb * per) * wpt;
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(QC_BLOCK), 0, st, (const uint16_t*)key, (int)key_st,
+                         (int)key_sh, (int)key_bytes, (const uint16_t*)value, (int)val_st, (int)val_sh, (int)val_bytes,
+                         k_cache, kc_sb, kc_sn, (int)kc_sh, v_cache, vc_sb, vc_sn, (int)vc_sh, (int)row_bytes,
+                         slot_mapping, (int)n_tokens, wpt, num_slots, lbs, k_scale, ks_pc, v_scale, vs_pc, k_mu);
+    };
+    if (head_dim == 128) go(quant_cache_rows_kernel<128>, resident_blocks<quant_cache_rows_kernel<128>>());
+    else go(quant_cache_rows_kernel<64>, resident_blocks<quant_cache_rows_kernel<64>>());
+    return launched("quant_cache");
+  }
+  if (num_heads * (head_dim / QC_CPL) > QC_BLOCK) return fail("quant_cache: at most %d heads of dim %lld", (int)(QC_BLOCK * QC_CPL / head_dim), (long long)head_dim);
+  const int ipt = H * (int)(head_dim / QC_CPL), tpb = QC_BLOCK / ipt;
+  const int64_t want = (n_tokens + tpb - 1) / tpb;
+  auto go = [&](auto kern, int resident) {
+    // one round of resident workgroups, balanced: the fewest tokens per lane that round allows, then
+    // just enough workgroups for n at that count
+    const int64_t conc = (int64_t)device_cus() * resident * tpb;   // tokens in flight
+    const int64_t per = (n_tokens + conc - 1) / conc;
+    const int grid = (int)std::min<int64_t>(want, (n_tokens + tpb * per - 1) / (tpb * per));
     hipLaunchKernelGGL(kern, dim3(grid), dim3(QC_BLOCK), 0, st, (const uint16_t*)key, key_st, key_sh,
                        (const uint16_t*)value, val_st, val_sh, k_cache, kc_sb, kc_sn, kc_sh, v_cache, vc_sb, vc_sn,
-                       vc_sh, slot_mapping, (int)n_tokens, H, num_slots, lbs, k_scale, (int)(k_scale_cols > 1),
-                       v_scale, (int)(v_scale_cols > 1), k_mu);
+                       vc_sh, slot_mapping, (int)n_tokens, H, num_slots, lbs, k_scale, ks_pc, v_scale, vs_pc, k_mu);
   };
-  if (head_dim == 128) go(quant_cache_kernel<128>);
-  else go(quant_cache_kernel<64>);
+  if (head_dim == 128) go(quant_cache_kernel<128>, resident_blocks<quant_cache_kernel<128>>());
+  else go(quant_cache_kernel<64>, resident_blocks<quant_cache_kernel<64>>());
   return launched("quant_cache");
 }
 

@@ -84,6 +84,36 @@ def test_quant_cache_matches_oracle(per_channel, D):
     assert torch.equal(kv_d.cpu(), kv)
 
 
+@pytest.mark.parametrize("H,D", [(8, 128), (12, 128), (32, 128), (16, 64), (2, 128), (1, 64)])
+@pytest.mark.parametrize("layout", ["interleaved", "separate"])
+def test_quant_cache_head_counts_and_packed_qkv(H, D, layout):
+    """Head counts whose channels fill 1, 2, 3 or 8 wavefronts per token (the wavefront-row kernel)
+    and fewer than one (the lane kernel); K/V are strided views of a packed qkv activation
+    [T, Hq + 2H, D], the cache vLLM's interleaved [nb, H, bs, 2D] or two separate [nb, bs, H, D]
+    caches. 7 padded rows at the end, every 13th slot -1; codes bit-exact. Slot 0 is never a target:
+    a padded row's store (which the wavefront-row kernel issues and the hardware drops) would land
+    there if it were not dropped."""
+    r = synth.rng(H * 1000 + D)
+    T, nb, bs, Hq = 300, 48, 16, 2 * H
+    qkv = synth.bf16(r.standard_normal((T + 7, Hq + 2 * H, D)) * 3)
+    key, value = qkv[:, Hq:Hq + H], qkv[:, Hq + H:]
+    slots = torch.from_numpy(1 + r.permutation(nb * bs - 1)[:T].astype(np.int64))
+    slots[::13] = -1
+    st = synth.scales_from(key[:T], value[:T], per_channel=(H % 2 == 0))
+    if layout == "interleaved":
+        kv = torch.zeros(nb, H, bs, 2 * D, dtype=torch.int8)
+        kc, vc = kv.transpose(1, 2).split(D, dim=-1)
+        kv_d = torch.zeros_like(kv, device=DEV)
+        kc_d, vc_d = kv_d.transpose(1, 2).split(D, dim=-1)
+    else:
+        kc, vc = torch.zeros(nb, bs, H, D, dtype=torch.int8), torch.zeros(nb, bs, H, D, dtype=torch.int8)
+        kc_d, vc_d = torch.zeros_like(kc, device=DEV), torch.zeros_like(vc, device=DEV)
+    O.quant_cache_ref(key, value, kc, vc, slots, st)
+    qkv_d = qkv.to(DEV)
+    ck.quant_reshape_and_cache(qkv_d[:, Hq:Hq + H], qkv_d[:, Hq + H:], kc_d, vc_d, dev(slots), dev(st))
+    assert torch.equal(kc_d.cpu(), kc) and torch.equal(vc_d.cpu(), vc)
+
+
 def test_quant_cache_c1_full_size_bit_exact():
     """BASELINE config c1: 16384 tokens x 4 x 128, ~2% padded slots, 4096 x 16 interleaved cache."""
     c = synth.c1_inputs()
