@@ -46,6 +46,8 @@ constexpr int MAX_SPLITS = 64;    // split_reduce_kernel keeps one split per lan
 constexpr int MAX_ROW_TILES = 4;  // row tiles (wavefronts) per attention workgroup
 constexpr int MIN_SPLIT_TILES = 4;  // shortest split: 4 tiles = 128 keys
 constexpr int DEFAULT_WAVES_PER_CU = 8;
+constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: skewed batches (c4's
+                                      // lengths; 10 x 32k + 86 x 1 keys) time best at 6-16
 constexpr int DEFAULT_PREFETCH = 3;
 constexpr int NUM_XCDS = 8;
 
@@ -481,6 +483,7 @@ struct AttnArgs {
   int waves;          // rt * ksplit wavefronts per workgroup
   int workers;        // workgroups of the attention grid
   int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
+  int seg_cost;       // work units a segment costs beyond its tiles (its fixed start and finish)
   int xcd_order;      // map workgroups to workers XCD by XCD
 };
 
@@ -505,51 +508,24 @@ __device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
   w.rgroups = (rt + a.rt - 1) / a.rt;
   return w;
 }
-// Length, in work units, of each of the request's (kv head, row group) segments: its tile count, or
+// Length, in work units, of each of the request's (kv head, row group) segments: seg_cost units for
+// its fixed cost (q load and quantization, the block-table walk's first round trips, the finish and
+// output write -- latency a one-tile segment pays as much as a long one), then one unit per tile; or
 // 1 when segments are never cut (no split buffers).
 __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
-  return a.max_splits == 1 ? (w.ntiles ? 1 : 0) : w.ntiles;
+  return a.max_splits == 1 ? (w.ntiles ? 1 : 0) : (w.ntiles ? a.seg_cost + w.ntiles : 0);
 }
 
 // The batch as one line of work units: request by request, kv head by kv head, row group by row
 // group. Workgroup w takes units [w * chunk, (w + 1) * chunk) (stream-K): every workgroup gets the
-// same amount of K/V to stream however skewed the request lengths are. chunk is also long enough that
-// no segment is cut into more than max_splits pieces. Both the attention and the merge kernel derive
-// it (whole wavefront, the same integer arithmetic), so they agree on every segment's pieces.
+// same amount of work -- K/V to stream plus the segments' fixed costs -- however skewed the request
+// lengths are. chunk is also long enough that no segment is cut into more than max_splits pieces.
+// The merge kernel needs none of it: it reads each segment's piece count from the denominators.
 struct Plan {
   long long total, chunk;
 };
-__device__ Plan make_plan(const AttnArgs& a, int lane, int before = 0, long long* units_before = nullptr) {
-  long long tot = 0, pre = 0;
-  int nmax = 0;
-  for (int r = lane; r < a.num_seqs; r += WAVE) {
-    const ReqWork w = req_work(a, r);
-    const int len = seg_units(a, w);
-    const long long u = (long long)len * a.hkv * w.rgroups;
-    tot += u;
-    if (r < before) pre += u;
-    nmax = max(nmax, len);
-  }
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    tot += __shfl_xor(tot, o, WAVE);
-    pre += __shfl_xor(pre, o, WAVE);
-    nmax = max(nmax, __shfl_xor(nmax, o, WAVE));
-  }
-  Plan p;
-  p.total = uniform64(tot);
-  long long c = (p.total + a.workers - 1) / a.workers;
-  if (a.max_splits > 1) {
-    c = max(c, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
-    c = max(c, (long long)a.min_tiles);
-  }
-  p.chunk = uniform64(max(c, 1ll));
-  if (units_before) *units_before = uniform64(pre);  // units of the requests before `before`
-  return p;
-}
-
-// make_plan and the search for the request holding unit `pos0` = worker * chunk, in one pass over the
-// requests (their work is read once; up to PLAN_CACHE * 64 requests stay in registers).
+// The plan (total units, chunk) and the search for the request holding unit `pos0` = worker * chunk,
+// in one pass over the requests (their work is read once; up to PLAN_CACHE * 64 requests stay in registers).
 constexpr int PLAN_CACHE = 4;
 __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_out, long long& start_out) {
   long long u[PLAN_CACHE];
@@ -1015,13 +991,19 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
     const int take = (int)min((long long)(seglen - off), end - pos);
-    const long long first = seg_start / pl.chunk, last = (seg_start + seglen - 1) / pl.chunk;
+    // the segment's first seg_cost units stand for its fixed cost, the rest for its tiles: pieces are
+    // the workers' shares of the tile units (a worker holding only fixed-cost units has no piece, and
+    // the pieces are numbered from the worker holding the first tile)
+    const int fc = whole ? 0 : a.seg_cost;
+    const long long first = (seg_start + fc) / pl.chunk, last = (seg_start + seglen - 1) / pl.chunk;
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
     const int row0 = (rg * a.rt + rtile) * 16;
-    const int c0 = whole ? 0 : off, c1 = whole ? w.ntiles : off + take;
+    const int c0 = whole ? 0 : max(off - fc, 0), c1 = whole ? w.ntiles : max(off + take - fc, 0);
     // a piece long enough for every key split to stream COOP_TILES tiles is split across them and
     // merged; shorter pieces go whole to one key split in turn (no barrier, no merge)
-    if (a.ksplit > 1 && c1 - c0 >= a.ksplit * COOP_TILES) {
+    if (c1 <= c0) {
+      // fixed-cost units only: nothing to stream here (uniform across the workgroup)
+    } else if (a.ksplit > 1 && c1 - c0 >= a.ksplit * COOP_TILES) {
       attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
                             (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
     } else {
@@ -1554,6 +1536,17 @@ int log2i(int64_t x) {
 }
 // Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
 // instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
+// Work units (32-key tiles of one workgroup's streaming) charged per segment for its fixed cost in
+// the stream-K partition (KVQ_SEG_COST overrides)
+int seg_cost_units() {
+  static const int c = [] {
+    const char* e = getenv("KVQ_SEG_COST");
+    const int v = e ? atoi(e) : DEFAULT_SEG_COST;
+    return v < 0 ? 0 : (v > 64 ? 64 : v);
+  }();
+  return c;
+}
+
 int prefetch_depth() {
   static const int depth = [] {
     const char* e = getenv("KVQ_PREFETCH");
@@ -1570,13 +1563,17 @@ int device_cus() {
   return cus;
 }
 
-// workgroups of QC_BLOCK threads of kernel K resident per CU at once (KVQ_QC_WG_PER_CU overrides)
+// workgroups of 256 threads of kernel K resident per CU at once (queried once); the environment
+// variable `env`, when set to a positive count, overrides it on every call (a tuning and test knob)
 template <auto K>
-int resident_blocks() {
+int resident_blocks(const char* env) {
+  if (const char* e = getenv(env)) {
+    const int v = atoi(e);
+    if (v > 0) return v;
+  }
   static const int nb = [] {
     int v = 0;
-    if (const char* e = getenv("KVQ_QC_WG_PER_CU")) v = atoi(e);
-    if (v <= 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, QC_BLOCK, 0) != hipSuccess || v <= 0)) v = QC_WAVES;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, QC_BLOCK, 0) != hipSuccess || v <= 0) v = QC_WAVES;
     return v;
   }();
   return nb;
@@ -1678,8 +1675,8 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
                          k_cache, kc_sb, kc_sn, (int)kc_sh, v_cache, vc_sb, vc_sn, (int)vc_sh, (int)row_bytes,
                          slot_mapping, (int)n_tokens, wpt, num_slots, lbs, k_scale, ks_pc, v_scale, vs_pc, k_mu);
     };
-    if (head_dim == 128) go(quant_cache_rows_kernel<128>, resident_blocks<quant_cache_rows_kernel<128>>());
-    else go(quant_cache_rows_kernel<64>, resident_blocks<quant_cache_rows_kernel<64>>());
+    if (head_dim == 128) go(quant_cache_rows_kernel<128>, resident_blocks<quant_cache_rows_kernel<128>>("KVQ_QC_WG_PER_CU"));
+    else go(quant_cache_rows_kernel<64>, resident_blocks<quant_cache_rows_kernel<64>>("KVQ_QC_WG_PER_CU"));
     return launched("quant_cache");
   }
   if (num_heads * (head_dim / QC_CPL) > QC_BLOCK) return fail("quant_cache: at most %d heads of dim %lld", (int)(QC_BLOCK * QC_CPL / head_dim), (long long)head_dim);
@@ -1695,8 +1692,8 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
                        (const uint16_t*)value, val_st, val_sh, k_cache, kc_sb, kc_sn, kc_sh, v_cache, vc_sb, vc_sn,
                        vc_sh, slot_mapping, (int)n_tokens, H, num_slots, lbs, k_scale, ks_pc, v_scale, vs_pc, k_mu);
   };
-  if (head_dim == 128) go(quant_cache_kernel<128>, resident_blocks<quant_cache_kernel<128>>());
-  else go(quant_cache_kernel<64>, resident_blocks<quant_cache_kernel<64>>());
+  if (head_dim == 128) go(quant_cache_kernel<128>, resident_blocks<quant_cache_kernel<128>>("KVQ_QC_WG_PER_CU"));
+  else go(quant_cache_kernel<64>, resident_blocks<quant_cache_kernel<64>>("KVQ_QC_WG_PER_CU"));
   return launched("quant_cache");
 }
 
@@ -1772,6 +1769,7 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
   a.max_splits = (int)num_splits; a.rt = rt; a.ksplit = ks; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES * ks;
+  a.seg_cost = seg_cost_units();
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   const int64_t tw = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
   a.workers = (int)std::max<int64_t>(1, std::min<int64_t>(tw / waves, INT32_MAX));
@@ -1820,8 +1818,8 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
   if (num_pages > INT32_MAX || num_blocks > INT32_MAX) return fail("dequant_pages: too many pages");
   if (num_pages * num_heads > (int64_t)INT32_MAX * 4 / 5) return fail("dequant_pages: too many pages");
   const int64_t units = num_pages * num_heads;
-  const int grid = (int)((units + 3) / 4);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int grid = (int)((units + 3) / 4);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(grid), dim3(4 * WAVE), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,
                        (int)num_blocks, (int)block_size, (int)num_heads, (uint16_t*)k_out, (uint16_t*)v_out,

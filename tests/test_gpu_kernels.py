@@ -363,6 +363,38 @@ def test_dequant_pages_vllm_layout():
     assert torch.equal(vo.cpu().view(torch.int16), vo_ref.view(torch.int16))
 
 
+def _random_pages(nb, bs, H, D, P, seed, per_channel):
+    """Random int8 caches [nb, bs, H, D], a one-row block table of P distinct random blocks, the
+    page list (request 0, pages 0..P-1) and scales."""
+    g = torch.Generator().manual_seed(seed)
+    kq = torch.randint(-127, 128, (nb, bs, H, D), generator=g, dtype=torch.int8)
+    vq = torch.randint(-127, 128, (nb, bs, H, D), generator=g, dtype=torch.int8)
+    bt = torch.randperm(nb, generator=g)[:P].to(torch.int32).reshape(1, P)
+    src_req, src_j = torch.zeros(P, dtype=torch.int32), torch.arange(P, dtype=torch.int32)
+    shape = (H, D) if per_channel else (H, 1)
+    st = {"k_scale": torch.rand(shape, generator=g) * 0.05 + 1e-3, "v_scale": torch.rand(shape, generator=g) * 0.05 + 1e-3,
+          "k_mu": torch.zeros(H, D)}
+    return kq, vq, bt, src_req, src_j, st
+
+
+def _check_dequant(kq, vq, bt, src_req, src_j, st):
+    ko_ref, vo_ref = O.dequant_pages_ref(kq, vq, bt, src_req, src_j, st)
+    P, (_, bs, H, D) = src_req.shape[0], kq.shape
+    ko = torch.full((P, bs, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    vo = nan_like(ko)
+    ck.ext().dequant_pages(dev(kq), dev(vq), ko, vo, dev(bt), dev(src_req), dev(src_j), dev(st["k_scale"]),
+                           dev(st["v_scale"]))
+    assert torch.equal(ko.cpu().view(torch.int16), ko_ref.view(torch.int16))
+    assert torch.equal(vo.cpu().view(torch.int16), vo_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("D,bs", [(128, 8), (128, 16), (128, 32), (64, 16), (64, 32), (64, 64), (128, 4), (64, 8)])
+def test_dequant_pages_block_sizes(D, bs):
+    """Block sizes from 4 to 64 rows at both head dims (one or several 4-row passes of the kernel per
+    page, a partial last pass at bs 8 / D 64); per-head scales at bs 16; bit-exact."""
+    _check_dequant(*_random_pages(400, bs, 4, D, 300, seed=bs * 7 + D, per_channel=(bs != 16)))
+
+
 def test_attention_on_vllm_interleaved_layout():
     c = synth.c0_case()
     kq, vq = int8_cache(c)
