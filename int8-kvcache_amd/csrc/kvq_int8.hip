@@ -141,12 +141,15 @@ __device__ __forceinline__ float wave_sum(float x) {
 // (lanes of a wavefront may hold different tokens). Both walk their tokens with a ring of loads in
 // flight.
 //
-// Codes: q0 = fl(x * r) with r = v_rcp_f32(s) (<= 1 ulp) is within 2^-22 * |q0| (<= 3.1e-5 for
-// |q0| <= 127.5) of fl(x / s). c = clamp(q0, +-127); t = fl(c + 1.5 * 2^23) holds rint(c) in its low mantissa bits,
-// so the code byte is read straight out of t, and the residual c - (t - 1.5 * 2^23) (exact) tells how
-// close c is to a rounding boundary. Lanes with a residual >= 0.5 - 2^-14 (6.1e-5, 2x the bound)
-// redo their 8 channels with IEEE division; below it rint(fl(x / s)) = rint(q0). Clamping first is
-// exact: rint(clamp(q, +-127)) = clamp(rint(q), +-127), and |q0| > 127 saturates either way.
+// Codes: with r = v_rcp_f32(s) (within 1 ulp of 1/s) and M = 1.5 * 2^23, t = fma(x, r, M) rounds
+// the exact product x * r once: t - M = rint(x * r) (ties to even) while |x * r| < 2^22, held in t's
+// low mantissa bits, so the code byte is read straight out of clamp(t, M +- 127). The exact x * r is
+// within 1.5 * 2^-23 * |x / s| (<= 2.3e-5 for |x / s| <= 127.5) of fl(x / s); e = fma(x, r, -(t - M))
+// = x * r - rint(x * r) (one rounding, 2^-25) tells how close it is to a rounding boundary. Lanes
+// with |e| >= 0.5 - 2^-14 (6.1e-5) redo their 8 channels with IEEE division; below it
+// rint(fl(x / s)) = rint(x * r), and clamping commutes with rint. |x * r| >= 2^22 means |x / s| >
+// 127.5: either e flags it or t clamps to +-127, the saturated code. Checked on the host over 6.7e9
+// (x, s, r) cases (tests/arith/quant_round_check.c).
 // ------------------------------------------------------------------------------------------------
 constexpr int QC_CPL = 8;     // channels per lane
 #ifndef QC_PF
@@ -154,7 +157,7 @@ constexpr int QC_CPL = 8;     // channels per lane
 #endif
 constexpr int QC_BLOCK = 256;
 #ifndef QC_WAVES
-#define QC_WAVES 4            // at least this many waves per SIMD (<= 128 VGPRs; the row kernel fits 5)
+#define QC_WAVES 4            // quant_cache_kernel: at least this many waves per SIMD (<= 128 VGPRs)
 #endif
 constexpr float QC_MAGIC = 12582912.0f;  // 1.5 * 2^23
 #ifndef QC_NT_LOAD
@@ -212,10 +215,10 @@ __device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], GetSc
   float worst = 0.f;
 #pragma unroll
   for (int e = 0; e < QC_CPL; ++e) {
-    const float c = sat127(x[e] * r[e]);
-    t[e] = c + QC_MAGIC;
-    const float res = c - (t[e] - QC_MAGIC);
+    const float t0 = __builtin_fmaf(x[e], r[e], QC_MAGIC);            // rint(x r) + M, one rounding
+    const float res = __builtin_fmaf(x[e], r[e], -(t0 - QC_MAGIC));   // x r - rint(x r)
     worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
+    t[e] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
   }
   if (worst >= 0.5f - 0x1p-14f) {  // rare: a quotient near a half-integer -- redo this lane exactly
     float sc[QC_CPL];
@@ -316,14 +319,18 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAV
 // exact pass reads its scales from LDS. The ring's waits then leave QC_ROW_PF - 1 tokens' loads and
 // the stores of earlier tokens in flight instead of draining them per token.
 #ifndef QC_ROW_PF
-#define QC_ROW_PF 5           // ring of token loads per wavefront (QC_ROW_PF - 1 in flight ahead)
+#define QC_ROW_PF 4           // ring of token loads per wavefront (QC_ROW_PF - 1 in flight ahead)
+#endif
+#ifndef QC_ROW_WAVES
+#define QC_ROW_WAVES 6        // waves per SIMD (<= 80 VGPRs): more wavefronts share the arithmetic left
+                              // after the last loads land
 #endif
 constexpr int QC_RSRC_WORD3 = 0x00020000;          // raw buffer, 32-bit dwords (gfx9 family)
 constexpr int QC_LOAD_AUX = QC_NT_LOAD ? 2 : 0;    // 2: nontemporal
 constexpr int QC_STORE_AUX = QC_NT_STORE ? 2 : 0;
 
 template <int D>
-__global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAVES))) void quant_cache_rows_kernel(
+__global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW_WAVES))) void quant_cache_rows_kernel(
     const uint16_t* __restrict__ key, int key_st, int key_sh, int key_bytes, const uint16_t* __restrict__ value,
     int val_st, int val_sh, int val_bytes, int8_t* __restrict__ kc, int64_t kc_sb, int64_t kc_sn, int kc_sh,
     int8_t* __restrict__ vc, int64_t vc_sb, int64_t vc_sn, int vc_sh, int row_bytes, const int64_t* __restrict__ slots,
