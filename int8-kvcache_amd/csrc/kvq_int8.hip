@@ -46,6 +46,8 @@ constexpr int MAX_SPLITS = 64;    // split_reduce_kernel keeps one split per lan
 constexpr int MAX_ROW_TILES = 4;  // row tiles (wavefronts) per attention workgroup
 constexpr int MIN_SPLIT_TILES = 4;  // shortest split: 4 tiles = 128 keys
 constexpr int DEFAULT_WAVES_PER_CU = 8;
+constexpr int DEFAULT_KSPLIT = 2;     // key splits per row tile: skewed batches (c4) run 9% faster
+                                      // than with 4 (2-wavefront workgroups, twice as many); c2 the same
 constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: skewed batches (c4's
                                       // lengths; 10 x 32k + 86 x 1 keys) time best at 6-16
 constexpr int DEFAULT_PREFETCH = 3;
@@ -624,7 +626,10 @@ __device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t 
 // denominator and accumulators in slot (k - 1) * rt + t, lane-major ([field][lane]: conflict-free).
 constexpr int MERGE_FIELDS = 36;  // 32 accumulators (D = 128), max, denominator, 2 spare
 constexpr int MERGE_SLOTS = MAX_ROW_TILES - 1;
-constexpr int COOP_TILES = 8;     // shortest share of a key split in a split piece, in 32-key tiles
+#ifndef KVQ_COOP_TILES
+#define KVQ_COOP_TILES 8
+#endif
+constexpr int COOP_TILES = KVQ_COOP_TILES;     // shortest share of a key split in a split piece, in 32-key tiles
 
 // One wavefront's share of one piece of a segment: its 16-row tile (rows row0..row0+15 of the
 // (token, q head) rows of kv head kvh) over the key tiles c_begin + ks, c_begin + ks + KS, ... below
@@ -960,13 +965,13 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   }
 }
 
-// Stream-K attention: workgroup w walks units [w * chunk, (w + 1) * chunk) of the batch (make_plan),
-// segment by segment. Its rt * ks wavefronts split each piece: rt consecutive 16-row tiles (they
-// stream the same K/V tiles at the same time -- the second and later reads hit L1/L2), each over ks
-// interleaved sets of key tiles merged through LDS at the end of the piece. Decode rows (one row
-// tile) use 4 key splits, so a workgroup covers 4x the keys of one wavefront and a long request's
-// (kv head) is cut across workgroups 4x less often (c2: never). Pieces too short for every key split
-// to stream COOP_TILES tiles are not split: the key splits take them in turn, each alone.
+// Stream-K attention: workgroup w walks units [w * chunk, (w + 1) * chunk) of the batch (the plan of
+// plan_and_locate), segment by segment. Its rt * ks wavefronts split each piece: rt consecutive
+// 16-row tiles (they stream the same K/V tiles at the same time -- the second and later reads hit
+// L1/L2), each over ks interleaved sets of key tiles merged through LDS at the end of the piece.
+// Decode rows (one row tile) use 2 key splits, so a workgroup covers 2x the keys of one wavefront and
+// a long request's (kv head) is cut across workgroups half as often. Pieces too short for every key
+// split to stream COOP_TILES tiles are not split: the key splits take them in turn, each alone.
 template <int D, int PF>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
@@ -1755,9 +1760,10 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   const int64_t maxq = std::min<int64_t>(std::max<int64_t>(max_query_len, 1), qmax);
   const int64_t row_tiles = ((int64_t)G * maxq + 15) / 16;
   const int rt = (int)std::min<int64_t>(MAX_ROW_TILES, row_tiles);
-  // key splits fill the workgroup's 4 wavefronts when the rows take fewer (KVQ_KSPLIT=1: none)
+  // key splits fill up to DEFAULT_KSPLIT wavefronts per row tile, within the workgroup's 4
+  // (KVQ_KSPLIT overrides, 1: none)
   const char* ks_env = getenv("KVQ_KSPLIT");
-  const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env))) : MAX_ROW_TILES;
+  const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env))) : DEFAULT_KSPLIT;
   const int ks = std::max(1, std::min(ks_max, MAX_ROW_TILES / rt));
   const int waves = rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535) return fail("int8_decode_attention: grid too large");
