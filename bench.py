@@ -146,12 +146,35 @@ def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
               "mean_abs": statistics.mean(e["mean_abs"] for e in errs),
               "rel_l2_max": max(e["rel_l2"] for e in errs), "bar": "max_abs<=2e-2, mean_abs<=2e-3"}
     parity["ok"] = parity["max_abs"] <= 2e-2 and parity["mean_abs"] <= 2e-3
+    parity["c0_bf16_drift"] = c0_drift(O)
     res = {"value": round(kv_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
            "sample": f"{n} whole c2 requests (32768 keys, 28/4/128) through the oracle's implementation B "
                      f"(float64) + run_paged on the host, {t_total:.1f} s; KV bytes / s",
            "us_per_request": round(t_total / n * 1e6, 1), "small_configs": cpu_small_configs(O, threads)}
     torch.set_num_threads(threads)
     return res, parity
+
+
+def c0_drift(O):
+    """The bf16-golden drift (kvq/ref_attn.py:93-102's compare against paged_attention_ref, fp32
+    attention over the original bf16 K/V) of the GPU kernel on c0, next to implementation B's own drift
+    and the kernel's distance from B. The int8 cache holds K - mu: that shifts every score of a row by
+    the same q . mu, so the softmax, and the comparison, are unchanged."""
+    c0 = synth.c0_case()
+    st = c0["static"]
+    kq = O.quantize(c0["k"].float() - st["k_mu"], st["k_scale"])
+    vq = O.quantize(c0["v"].float(), st["v_scale"])
+    scale = 128 ** -0.5
+    args = (c0["cu"], c0["seq_lens"], c0["block_table"], scale)
+    b = O.paged_static_attention(O.CFG32_Q32, st, True, 8)(c0["q"].float(), kq, vq, *args)
+    gold = O.paged_attention_ref(c0["q"], c0["k"], c0["v"], *args)
+    out = torch.empty(c0["q"].shape, dtype=torch.bfloat16, device=DEV)
+    ck.decode_attention(c0["q"].to(DEV), kq.to(DEV), vq.to(DEV), out, c0["cu"].to(DEV), c0["seq_lens"].to(DEV),
+                        c0["block_table"].to(DEV), scale, {k: v.to(DEV) for k, v in st.items()})
+    o = out.cpu()
+    rnd = lambda e: {k: round(float(v), 6) for k, v in e.items()}
+    return {"kernel_vs_B": rnd(O.compare(b, o)), "kernel_vs_bf16_golden": rnd(O.compare(gold, o)),
+            "B_vs_bf16_golden": rnd(O.compare(gold, b))}
 
 
 def cpu_small_configs(O, threads, reps=5):
