@@ -629,7 +629,8 @@ constexpr int MERGE_SLOTS = MAX_ROW_TILES - 1;
 #ifndef KVQ_COOP_TILES
 #define KVQ_COOP_TILES 8
 #endif
-constexpr int COOP_TILES = KVQ_COOP_TILES;     // shortest share of a key split in a split piece, in 32-key tiles
+constexpr int COOP_TILES = KVQ_COOP_TILES;
+constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference maximum     // shortest share of a key split in a split piece, in 32-key tiles
 
 // One wavefront's share of one piece of a segment: its 16-row tile (rows row0..row0+15 of the
 // (token, q head) rows of kv head kvh) over the key tiles c_begin + ks, c_begin + ks + KS, ... below
@@ -815,7 +816,11 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     mx = group4_max(mx);
     // an int8 dot product never reaches INT32_MIN: it marks a row with no visible key in the tile
     const float tmax = (MASKED && mx == INT32_MIN) ? -INFINITY : (float)mx * rs;
-    const float mnew = __builtin_fmaxf(m, tmax);
+    // m is a reference maximum, raised only when a tile's maximum exceeds it by ATTN_SLACK (log2
+    // units): P = 2^(s - m) <= 2^ATTN_SLACK, and acc / l are rescaled in few tiles. The P codes are
+    // rint(127 P / max P) of the tile, the same for any reference; only ps carries it.
+    const bool raise = tmax > m + ATTN_SLACK;
+    const float mnew = raise ? tmax : m;
     const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     m = mnew;
     const float pm = __builtin_amdgcn_exp2f(tmax - mnew);  // max of this tile's P (exp2 is monotone)
@@ -838,7 +843,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     // sum of the 8 codes (v_sad_u8: sum of |byte - 0|)
     const float psum = (float)__builtin_amdgcn_sad_u8(p1, 0u, __builtin_amdgcn_sad_u8(p0, 0u, 0u));
     l = __builtin_fmaf(psum, ps, l * alpha);
-    if (__any(alpha != 1.f)) {
+    if (__any(raise)) {
 #pragma unroll
       for (int t = 0; t < VT; ++t)
 #pragma unroll
