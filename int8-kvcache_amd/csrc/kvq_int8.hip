@@ -48,6 +48,7 @@ constexpr int MIN_SPLIT_TILES = 4;  // shortest split: 4 tiles = 128 keys
 constexpr int DEFAULT_WAVES_PER_CU = 8;
 constexpr int DEFAULT_KSPLIT = 2;     // key splits per row tile: skewed batches (c4) run 9% faster
                                       // than with 4 (2-wavefront workgroups, twice as many); c2 the same
+constexpr int DEFAULT_LDS_PREFETCH = 3;   // shared LDS ring slots (3, 4 and 6 time the same on c3)
 constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: skewed batches (c4's
                                       // lengths; 10 x 32k + 86 x 1 keys) time best at 6-16
 constexpr int DEFAULT_PREFETCH = 3;
@@ -493,6 +494,8 @@ struct AttnArgs {
   int workers;        // workgroups of the attention grid
   int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
   int seg_cost;       // work units a segment costs beyond its tiles (its fixed start and finish)
+  int lds_ring;       // 1: the workgroup's wavefronts are row tiles of the same rows (ksplit 1, rt >= 2)
+                      // and share each K/V tile through an LDS ring of PF slots (the dynamic LDS)
   int xcd_order;      // map workgroups to workers XCD by XCD
 };
 
@@ -603,6 +606,21 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
 __device__ __forceinline__ i32x4 ldk(const i32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ u32x2 ldv(const u32x2* p) { return __builtin_nontemporal_load(p); }
 
+// s_waitcnt that waits until at most n vector-memory operations of this wavefront are outstanding
+// (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+// workgroup barrier that orders LDS only (a plain __syncthreads would also drain every global load in
+// flight, which the LDS rings below keep outstanding on purpose)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 template <int D>
 struct KVTile {
   i32x4 k[2][D / 64];     // QK A operands: keys 16b + m, bytes = channels (D/4) g + 16 s + j
@@ -638,7 +656,7 @@ constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference
 // wavefront ks = 0 finishes the piece, the segment's `part`-th of `nparts`: a whole segment writes
 // bf16 out, a cut one an fp32 partial. Every wavefront of the workgroup calls this for every piece
 // (inactive ones -- row tiles past the request's rows -- only join the barriers of the merge).
-template <int D, int PF>
+template <int D, int PF, bool SHARED>
 __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
                                                int c_begin, int c_end, int ks, int KS, int rtile, bool active,
                                                int part, int nparts, float* lds, int lane) {
@@ -663,7 +681,11 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   const int n = lane & 15, g = lane >> 4;
   const int G = a.G;
   const int L = a.seq_lens[seq];
-  if (L <= 0 || !active) c_end = c_begin;  // no keys (malformed) or no rows: nothing is read
+  // no keys (malformed): nothing is read. A wavefront with no rows reads nothing either -- except
+  // with a shared LDS ring, where it still fetches its share of every tile and keeps the barriers
+  constexpr bool shared = SHARED;  // launched with a.lds_ring set
+  const bool work = L > 0 && active;
+  if (L <= 0 || (!active && !shared)) c_end = c_begin;
   // this wavefront's tiles: c_begin + ks + j * KS, j < nt
   const int nt = c_begin + ks < c_end ? (c_end - c_begin - ks + KS - 1) / KS : 0;
   auto tile = [&](int j) { return c_begin + ks + j * KS; };
@@ -722,10 +744,129 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     }
   };
 
-  KVTile<D> ring[PF];
-  if (nt > 0) {
+  // ---- shared ring: a tile is DMA'd once (global_load_lds_dwordx4, 64 lanes x 16 bytes = RPI rows
+  // per instruction; K rows, then V rows, each row's 16-byte chunks XOR-swizzled by row % CHR so
+  // that the operand reads below spread over the banks); the rt wavefronts issue instruction
+  // rtile + rt u of each tile (u < NIW; past NI an instruction is issued twice -- the same bytes to
+  // the same place) ----
+  constexpr int RB_ = D;                     // bytes per K (or V) row
+  constexpr int CHR = RB_ / 16;              // 16-byte chunks per row
+  constexpr int RPI = WAVE / CHR;            // rows per DMA instruction
+  constexpr int NI = 2 * TILE / RPI;         // DMA instructions per tile (K rows, then V rows)
+  constexpr int SLOT = 2 * TILE * RB_;       // bytes per ring slot
+  uint8_t* lring = reinterpret_cast<uint8_t*>(lds);
+  auto dma = [&](auto niw_t, int c, int st) {
+    constexpr int NIW = decltype(niw_t)::value;
+    const int n0 = c * TILE, n1 = n0 + 16;
+    const int p0 = page_of(n0);
+    const int p1 = n1 < L ? page_of(n1) : p0;
+    const int o0 = n0 & (bs - 1), o1 = n1 < L ? (n1 & (bs - 1)) : o0;
 #pragma unroll
-    for (int j = 0; j < PF - 1; ++j) load(ring[j], tile(min(j, nt - 1)));
+    for (int u = 0; u < NIW; ++u) {
+      int i = rtile + a.rt * u;
+      if (i >= NI) i -= NI;
+      const bool isv = i >= NI / 2;
+      const int blk = i % (NI / 2);
+      const int row = RPI * blk + lane / CHR;  // rows of one instruction sit in one half of the tile
+      const int lc = (lane % CHR) ^ (row % CHR);
+      const bool hi = row >= 16;
+      const int p = hi ? p1 : p0, o = hi ? o1 + row - 16 : o0 + row;
+      const int8_t* src = isv ? vbase + (int64_t)p * a.v_sb + (int64_t)o * a.v_sn + 16 * lc
+                              : kbase + (int64_t)p * a.k_sb + (int64_t)o * a.k_sn + 16 * lc;
+      __builtin_amdgcn_global_load_lds((const void*)src,
+                                       (__attribute__((address_space(3))) void*)(lring + st * SLOT + (isv ? TILE * RB_ : 0) + 1024 * blk),
+                                       16, 0, 0);
+    }
+  };
+  // this lane's operands of slot st, as load() would put them in registers: K row 16 b + n, logical
+  // chunk (KPL / 16) g + s; V rows 4 g + i (i < 4) and 16 + 4 g + i - 4, bytes VT n .. VT n + VT - 1.
+  // Inline assembly, each statement waiting for its own reads: the compiler would otherwise make the
+  // reads wait for every DMA in flight (it cannot tell they read another slot).
+  auto lds_tile = [&](int st, KVTile<D>& r) {
+    const uint32_t kb = (uint32_t)(uintptr_t)(lring + st * SLOT), vb = kb + TILE * RB_;
+    uint32_t ka[2][KSTEPS], va[8];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int s2 = 0; s2 < KSTEPS; ++s2) {
+        const int row = 16 * b + n;
+        ka[b][s2] = kb + row * RB_ + 16 * (((KPL / 16) * g + s2) ^ (row % CHR));
+      }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = i < 4 ? 4 * g + i : 16 + 4 * g + i - 4;
+      const int byte = VT * n;
+      va[i] = vb + row * RB_ + 16 * ((byte / 16) ^ (row % CHR)) + byte % 16;
+    }
+    if constexpr (D == 128) {
+      typedef unsigned long long u64;
+      u64 w[8];
+      asm volatile(
+          "ds_read_b128 %0, %12\n"
+          "ds_read_b128 %1, %13\n"
+          "ds_read_b128 %2, %14\n"
+          "ds_read_b128 %3, %15\n"
+          "ds_read_b64 %4, %16\n"
+          "ds_read_b64 %5, %17\n"
+          "ds_read_b64 %6, %18\n"
+          "ds_read_b64 %7, %19\n"
+          "ds_read_b64 %8, %20\n"
+          "ds_read_b64 %9, %21\n"
+          "ds_read_b64 %10, %22\n"
+          "ds_read_b64 %11, %23\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(r.k[0][0]), "=&v"(r.k[0][1]), "=&v"(r.k[1][0]), "=&v"(r.k[1][1]), "=&v"(w[0]), "=&v"(w[1]),
+            "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
+          : "v"(ka[0][0]), "v"(ka[0][1]), "v"(ka[1][0]), "v"(ka[1][1]), "v"(va[0]), "v"(va[1]), "v"(va[2]),
+            "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7])
+          : "memory");
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        r.v[i][0] = (uint32_t)w[i];
+        r.v[i][1] = (uint32_t)(w[i] >> 32);
+      }
+    } else {
+      uint32_t w[8];
+      asm volatile(
+          "ds_read_b128 %0, %10\n"
+          "ds_read_b128 %1, %11\n"
+          "ds_read_b32 %2, %12\n"
+          "ds_read_b32 %3, %13\n"
+          "ds_read_b32 %4, %14\n"
+          "ds_read_b32 %5, %15\n"
+          "ds_read_b32 %6, %16\n"
+          "ds_read_b32 %7, %17\n"
+          "ds_read_b32 %8, %18\n"
+          "ds_read_b32 %9, %19\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(r.k[0][0]), "=&v"(r.k[1][0]), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]),
+            "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
+          : "v"(ka[0][0]), "v"(ka[1][0]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]),
+            "v"(va[6]), "v"(va[7])
+          : "memory");
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r.v[i][0] = w[i];
+    }
+  };
+  const int niw = (NI + a.rt - 1) / a.rt;    // DMA instructions per wavefront and tile (uniform)
+  auto with_niw = [&](auto f) {             // f(std::integral_constant<int, NIW>)
+    if (niw == 1) f(std::integral_constant<int, 1>{});
+    else if (niw == 2) f(std::integral_constant<int, 2>{});
+    else if (niw == 3) f(std::integral_constant<int, 3>{});
+    else f(std::integral_constant<int, 4>{});
+  };
+
+  KVTile<D> ring[SHARED ? 1 : PF];  // the register ring (unused with the LDS ring)
+  if (nt > 0) {
+    if constexpr (SHARED) {
+      with_niw([&](auto niw_t) {
+#pragma unroll
+        for (int j = 0; j < PF - 1; ++j) dma(niw_t, tile(min(j, nt - 1)), j);
+      });
+    } else {
+#pragma unroll
+      for (int j = 0; j < PF - 1; ++j) load(ring[j], tile(min(j, nt - 1)));
+    }
   }
 
   // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
@@ -865,7 +1006,29 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   // prologue. Tiles below full_end have no masked key for any row of the wavefront; the first loop
   // runs whole rounds of them (j < j_full), the second the rest -- both start rounds at j = k * PF,
   // so the ring slot of every tile is a compile-time index. ----
-  if (nt > 0) {
+  if constexpr (SHARED) {
+   if (nt > 0) {
+    // one barrier per tile: this wavefront's DMA of tile j has landed (wait), everyone's has and
+    // everyone is done reading tile j - 1 (barrier), so its slot takes tile j + PF - 1
+    const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
+    with_niw([&](auto niw_t) {
+      constexpr int NIW = decltype(niw_t)::value;
+      KVTile<D> cur;
+      for (int j = 0; j < nt; ++j) {
+        wait_vm<(PF - 2) * NIW>();
+        lds_barrier();
+        dma(niw_t, tile(min(j + PF - 1, nt - 1)), (j + PF - 1) % PF);
+        if (work) {
+          lds_tile(j % PF, cur);
+          if (tile(j) < full_end) compute(std::false_type{}, cur, tile(j));
+          else compute(std::true_type{}, cur, tile(j));
+        }
+      }
+    });
+    wait_vm<0>();   // the ring is empty and read before the next piece refills it
+    lds_barrier();
+   }
+  } else if (nt > 0) {
     const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
     const int j_full = min(nt, full_end > c_begin + ks ? (full_end - c_begin - ks + KS - 1) / KS : 0);
     int j0 = 0;
@@ -977,7 +1140,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
 // Decode rows (one row tile) use 2 key splits, so a workgroup covers 2x the keys of one wavefront and
 // a long request's (kv head) is cut across workgroups half as often. Pieces too short for every key
 // split to stream COOP_TILES tiles are not split: the key splits take them in turn, each alone.
-template <int D, int PF>
+template <int D, int PF, bool SHARED = false>
 __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // the wavefront index is uniform across the wavefront: keep it (and all row bookkeeping) scalar
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1021,11 +1184,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (c1 <= c0) {
       // fixed-cost units only: nothing to stream here (uniform across the workgroup)
     } else if (a.ksplit > 1 && c1 - c0 >= a.ksplit * COOP_TILES) {
-      attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
+      attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
                             (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
     } else {
       if (solo % a.ksplit == kspl)
-        attend_segment<D, PF>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, 0, 1, rtile, row0 < w.qlen * a.G,
+        attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, 0, 1, rtile, row0 < w.qlen * a.G,
                               (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
       ++solo;
     }
@@ -1215,20 +1378,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
   return *reinterpret_cast<uint32_t*>(&h);
 }
 
-// s_waitcnt that waits until at most n vector-memory operations of this wavefront are outstanding
-// (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt 6:4 and lgkmcnt 11:8 left at "no wait")
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-// workgroup barrier that orders LDS only (a plain __syncthreads would also drain every global load in
-// flight, which the LDS ring below keeps outstanding on purpose)
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
@@ -1564,6 +1713,16 @@ int seg_cost_units() {
   return c;
 }
 
+// slots of the attention's shared LDS ring (KVQ_LDS_PREFETCH: 3, 4 or 6)
+int lds_prefetch_depth() {
+  static const int depth = [] {
+    const char* e = getenv("KVQ_LDS_PREFETCH");
+    const int v = e ? atoi(e) : DEFAULT_LDS_PREFETCH;
+    return v <= 3 ? 3 : (v >= 6 ? 6 : 4);
+  }();
+  return depth;
+}
+
 int prefetch_depth() {
   static const int depth = [] {
     const char* e = getenv("KVQ_PREFETCH");
@@ -1797,9 +1956,23 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   g_ev_start = g_ev_stop = nullptr;
   if (ev0) (void)hipEventRecord(ev0, st);
   const dim3 block(WAVE * waves);
-  const size_t lds = (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
-  const int pf = prefetch_depth();
-  if (head_dim == 128) {
+  // row tiles of the same rows without key splits share each K/V tile through an LDS ring
+  // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
+  a.lds_ring = (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0)) ? 1 : 0;
+  const int pf = a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
+  const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
+                                : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
+  if (a.lds_ring) {
+    if (head_dim == 128) {
+      if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3, true>), grid, block, lds, st, a);
+      else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6, true>), grid, block, lds, st, a);
+      else hipLaunchKernelGGL((attn_kernel<128, 4, true>), grid, block, lds, st, a);
+    } else {
+      if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3, true>), grid, block, lds, st, a);
+      else if (pf == 6) hipLaunchKernelGGL((attn_kernel<64, 6, true>), grid, block, lds, st, a);
+      else hipLaunchKernelGGL((attn_kernel<64, 4, true>), grid, block, lds, st, a);
+    }
+  } else if (head_dim == 128) {
     if (pf == 2) hipLaunchKernelGGL((attn_kernel<128, 2>), grid, block, lds, st, a);
     else if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3>), grid, block, lds, st, a);
     else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6>), grid, block, lds, st, a);
