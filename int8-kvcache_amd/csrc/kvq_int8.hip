@@ -613,13 +613,11 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
-// workgroup barrier that orders LDS only (a plain __syncthreads would also drain every global load in
-// flight, which the LDS rings below keep outstanding on purpose)
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// workgroup barrier for the LDS DMA rings below: this wavefront's LDS reads have returned, then
+// s_barrier, with a compiler-level memory barrier around it. Each wavefront waits for its own DMAs
+// (wait_vm) before it; a __syncthreads, or a release fence on LDS, would also wait for every DMA in
+// flight (they write LDS), which the rings keep outstanding on purpose.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int D>
 struct KVTile {
@@ -1366,8 +1364,8 @@ constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
 constexpr int PR_ROWS = 4 * 16 * PR_RB;     // rows per workgroup (4 wavefronts)
 constexpr int PR_KEYS = 32;                 // keys per tile
 constexpr float PR_SLACK = 8.f;             // log2 headroom of the reference maximum (general loop)
-constexpr float PR_FAST_SLACK = 64.f;       // largest excess over a row's first-tile maximum the fast pass takes
-constexpr int PR_STAGES = 4;                // LDS ring: tiles in flight + the one computed
+constexpr float PR_FAST_PSUM_MAX = 0x1p60f;  // largest per-lane P sum the fast pass takes (P <= 2^60)
+constexpr int PR_STAGES = 3;                // LDS ring: tiles in flight + the one computed (3 x 16 KB: 3 workgroups per CU)
 
 // two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
@@ -1380,7 +1378,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
 
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   constexpr int DS = D / 32;                // 32-channel chunks of the QK contraction
   constexpr int VT = D / 16;                // PV channel tiles
   constexpr int RB = PR_RB;
@@ -1434,18 +1432,21 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   }
 
   // ---- DMA of tile c into ring stage st: wavefront w's instruction i fills key rows
-  // RPI * (IPW * w + i) .. + RPI - 1 of each matrix, lane l the physical chunk l % CH of row l / CH. The
-  // lane's part of the source address is fixed for the launch (kvh, channel chunk); the rows' pages are
-  // two scalar loads per tile (a 32-key tile spans at most two pages, block size >= 16). ----
+  // RPI * (IPW * w + i) .. + RPI - 1 of each matrix, lane l the physical chunk l % CH of row l / CH.
+  // Those RPI rows lie in one page (32-key tiles start at multiples of 32, block size >= 16), so
+  // the instruction's page and row are a scalar base and the lane's offset from it (row, swizzled
+  // chunk) is fixed for the launch: an SGPR base plus a VGPR offset, no per-lane address arithmetic.
+  // Rows past the last key read rows of a valid page; the causal mask drops them. ----
   const int bsm = (1 << a.lbs) - 1;
-  uint32_t kl[IPW], vl[IPW];   // byte offsets of the lane's chunk inside a key row of head kvh
-  int lrow[IPW];
+  uint32_t kvo[IPW], vvo[IPW];   // byte offsets of the lane's chunk from its instruction's first row
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
-    lrow[i] = RPI * (IPW * wave + i) + lane / CH;
-    kl[i] = 2u * (uint32_t)(kvh * a.k_sh + 8 * ((lane % CH) ^ kswz(lrow[i])));
-    vl[i] = 2u * (uint32_t)(kvh * a.v_sh + 8 * ((lane % CH) ^ vswz(lrow[i])));
+    const int lr = lane / CH, row = RPI * (IPW * wave + i) + lr;
+    kvo[i] = (uint32_t)(2 * lr * a.k_sn + 16 * ((lane % CH) ^ kswz(row)));
+    vvo[i] = (uint32_t)(2 * lr * a.v_sn + 16 * ((lane % CH) ^ vswz(row)));
   }
+  const char* kh = (const char*)(a.kc + (int64_t)kvh * a.k_sh);
+  const char* vh = (const char*)(a.vc + (int64_t)kvh * a.v_sh);
   auto issue = [&](int c, int st) {
     c = min(c, max(ntiles - 1, 0));  // past the end: reload the last tile into the free stage
     const int kb0 = c * PR_KEYS, klast = max(kend - 1, 0);
@@ -1454,19 +1455,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     int p1 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i1]);
     p0 = (p0 >= 0 && p0 < a.num_blocks) ? p0 : 0;
     p1 = (p1 >= 0 && p1 < a.num_blocks) ? p1 : 0;
-    const char* kp0 = (const char*)(a.kc + (int64_t)p0 * a.k_sb);
-    const char* kp1 = (const char*)(a.kc + (int64_t)p1 * a.k_sb);
-    const char* vp0 = (const char*)(a.vc + (int64_t)p0 * a.v_sb);
-    const char* vp1 = (const char*)(a.vc + (int64_t)p1 * a.v_sb);
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const int key = min(kb0 + lrow[i], klast);       // rows past the last key re-read a valid one
-      const bool second = (key >> a.lbs) != i0;
-      const uint32_t slot = (uint32_t)(key & bsm);
-      const char* ks = (second ? kp1 : kp0) + (slot * 2u * (uint32_t)a.k_sn + kl[i]);
-      const char* vs = (second ? vp1 : vp0) + (slot * 2u * (uint32_t)a.v_sn + vl[i]);
-      __builtin_amdgcn_global_load_lds((const void*)ks, (__attribute__((address_space(3))) void*)(ring[st][0] + 1024 * (IPW * wave + i)), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)vs, (__attribute__((address_space(3))) void*)(ring[st][1] + 1024 * (IPW * wave + i)), 16, 0, 0);
+      const int key0 = kb0 + RPI * (IPW * wave + i);
+      const int64_t pg = (key0 >> a.lbs) != i0 ? p1 : p0;
+      const int64_t slot0 = key0 & bsm;
+      const char* kb = kh + 2 * (pg * a.k_sb + slot0 * a.k_sn);   // scalar: the instruction's first row
+      const char* vb = vh + 2 * (pg * a.v_sb + slot0 * a.v_sn);
+      __builtin_amdgcn_global_load_lds((const void*)(kb + (uint64_t)kvo[i]),
+                                       (__attribute__((address_space(3))) void*)(ring[st][0] + 1024 * (IPW * wave + i)), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vb + (uint64_t)vvo[i]),
+                                       (__attribute__((address_space(3))) void*)(ring[st][1] + 1024 * (IPW * wave + i)), 16, 0, 0);
     }
   };
   // V^T transposing reads: this lane supplies the address of row vr0 = 4 g + n / 4 (keys 0..15 half) and
@@ -1493,20 +1492,45 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   // ---- per tile: scores (QK) and each row's largest, masked for the keys past a row's limit ----
   f32x4 sc[RB][2];
   float lmax[RB], top[RB];
+  // K operand reads from inline assembly, each statement waiting for its own reads: as plain loads
+  // the compiler makes them wait for every LDS DMA in flight (it cannot tell they read another ring
+  // stage), which would empty the ring every tile
   auto scores = [&](int st, int c) {
     const int n0 = c * PR_KEYS;
-    const uint8_t* kb = ring[st][0];
+    const uint32_t kb = (uint32_t)(uintptr_t)(ring[st][0]);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       const int row = 16 * b + n;
+      uint32_t ad[DS];
 #pragma unroll
-      for (int s = 0; s < DS; ++s) {
-        const bf16x8 kop = *reinterpret_cast<const bf16x8*>(kb + row * ROWB + 16 * ((4 * s + g) ^ kswz(row)));
+      for (int s = 0; s < DS; ++s) ad[s] = kb + row * ROWB + 16 * ((4 * s + g) ^ kswz(row));
+      bf16x8 kop[DS];
+      if constexpr (DS == 4) {
+        asm volatile(
+            "ds_read_b128 %0, %4\n"
+            "ds_read_b128 %1, %5\n"
+            "ds_read_b128 %2, %6\n"
+            "ds_read_b128 %3, %7\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(kop[0]), "=&v"(kop[1]), "=&v"(kop[2]), "=&v"(kop[3])
+            : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+            : "memory");
+      } else {
+        static_assert(DS == 2, "head_dim 128 or 64");
+        asm volatile(
+            "ds_read_b128 %0, %2\n"
+            "ds_read_b128 %1, %3\n"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(kop[0]), "=&v"(kop[1])
+            : "v"(ad[0]), "v"(ad[1])
+            : "memory");
+      }
+#pragma unroll
+      for (int s = 0; s < DS; ++s)
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
-          sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop, qop[rb][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][b],
+          sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[s], qop[rb][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][b],
                                                              0, 0, 0);
-      }
     }
     if (n0 + PR_KEYS > lim_lo) {  // a tile on the causal edge of some row of the wavefront
 #pragma unroll
@@ -1548,6 +1572,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
       for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
     }
   };
+  bool jump = false;  // per lane: a tile's P summed past PR_FAST_PSUM_MAX (only the fast pass reads it)
   auto softmax_pv = [&](int st) {
     bf16x8 pop[RB];
 #pragma unroll
@@ -1560,6 +1585,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
           p[b][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[rb][b][i], a.sm_log2, -m[rb]));
           psum += p[b][i];
         }
+      // unflagged, every P of the lane is <= 2^60 (far from any fp32 / bf16 overflow in P, l or acc);
+      // a score more than 60 above the reference (log2 units) makes its P, hence the sum, exceed it
+      jump |= !(psum <= PR_FAST_PSUM_MAX);
       l[rb] += psum;
       u32x4 pw;
       pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
@@ -1613,18 +1641,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
     };
     // Fast pass: tile 0 sets each row's reference maximum (acc is still zero), later tiles only
     // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
-    // exceeds the reference by 2^PR_FAST_SLACK; a row where one does is only flagged here -- acc is
-    // never changed under a condition, which keeps the accumulators in place in registers.
+    // exceeds the reference by more than 60 (log2 units); a lane whose P sum says one did is only
+    // flagged (in softmax_pv) -- acc is never changed under a condition, which keeps the accumulators
+    // in place in registers.
     next_tile(0);
     row_top();
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
     softmax_pv(0);
-    bool jump = false;  // per lane: one of its scores exceeded the row's reference by 2^PR_FAST_SLACK
+    jump = false;
     for (int c = 1; c < ntiles; ++c) {
       next_tile(c);
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) jump |= lmax[rb] * a.sm_log2 > m[rb] + PR_FAST_SLACK;
       softmax_pv(c % NS);
     }
     wait_vm<0>();
