@@ -69,8 +69,8 @@ int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, i
  * Requests with q_len == 0 or q_len > qmax are skipped (their out rows untouched).
  * Work is split stream-K: the batch is one line of units -- request by request, kv head by kv head,
  * group of up to four 16-row tiles of (token, q head) rows, then 32-key tile -- and each of about
- * target_waves / 4 workgroups of up to four wavefronts (target_waves 0 = 8 wavefronts per compute
- * unit) takes an equal contiguous range of it; the wavefronts of a workgroup split a range by row
+ * target_waves / w workgroups of w <= 4 wavefronts (target_waves 0 = as many wavefronts as the chosen
+ * kernel keeps resident on the device) takes an equal contiguous range of it; the wavefronts of a workgroup split a range by row
  * tile and, for short queries, by interleaved key tiles merged in LDS. A (request, kv head, row
  * group) that one workgroup covers whole writes out directly; one that is cut writes fp32 pieces to
  * segm_out [T, Hq, S, D] and segm_max / segm_sum [T, Hq, S] (element (t, h, s) at

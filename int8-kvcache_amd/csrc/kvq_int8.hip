@@ -29,7 +29,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 #include <type_traits>
 
 #include "../../include/kvq_int8.h"
@@ -753,6 +756,11 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   constexpr int NI = 2 * TILE / RPI;         // DMA instructions per tile (K rows, then V rows)
   constexpr int SLOT = 2 * TILE * RB_;       // bytes per ring slot
   uint8_t* lring = reinterpret_cast<uint8_t*>(lds);
+  // lane part of a DMA source address: row lane / CHR of the instruction's RPI rows, chunk lc. The
+  // swizzle row % CHR is (lane / CHR) % CHR whatever the instruction (RPI is a multiple of CHR), so the
+  // offsets are the same for every instruction; the rest of the address is uniform (scalar base).
+  const uint32_t lrow = lane / CHR, lch = 16 * ((lane % CHR) ^ (lrow % CHR));
+  const uint32_t kdo = lrow * (uint32_t)a.k_sn + lch, vdo = lrow * (uint32_t)a.v_sn + lch;
   auto dma = [&](auto niw_t, int c, int st) {
     constexpr int NIW = decltype(niw_t)::value;
     const int n0 = c * TILE, n1 = n0 + 16;
@@ -765,13 +773,11 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
       if (i >= NI) i -= NI;
       const bool isv = i >= NI / 2;
       const int blk = i % (NI / 2);
-      const int row = RPI * blk + lane / CHR;  // rows of one instruction sit in one half of the tile
-      const int lc = (lane % CHR) ^ (row % CHR);
-      const bool hi = row >= 16;
-      const int p = hi ? p1 : p0, o = hi ? o1 + row - 16 : o0 + row;
-      const int8_t* src = isv ? vbase + (int64_t)p * a.v_sb + (int64_t)o * a.v_sn + 16 * lc
-                              : kbase + (int64_t)p * a.k_sb + (int64_t)o * a.k_sn + 16 * lc;
-      __builtin_amdgcn_global_load_lds((const void*)src,
+      const bool hi = RPI * blk >= 16;  // rows of one instruction sit in one half of the tile
+      const int p = hi ? p1 : p0, o = (hi ? o1 - 16 : o0) + RPI * blk;
+      const int8_t* sb = isv ? vbase + (int64_t)p * a.v_sb + (int64_t)o * a.v_sn
+                             : kbase + (int64_t)p * a.k_sb + (int64_t)o * a.k_sn;
+      __builtin_amdgcn_global_load_lds((const void*)(sb + (uint64_t)(isv ? vdo : kdo)),
                                        (__attribute__((address_space(3))) void*)(lring + st * SLOT + (isv ? TILE * RB_ : 0) + 1024 * blk),
                                        16, 0, 0);
     }
@@ -987,8 +993,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
       for (int t = 0; t < VT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][i] *= alpha;
-    }
-    // ---- PV: O^T[channel][row] += (V^T . P^T) * ps ----
+    }    // ---- PV: O^T[channel][row] += (V^T . P^T) * ps ----
 #pragma unroll
     for (int t = 0; t < VT; ++t) {
       i32x4 z = {0, 0, 0, 0};
@@ -1008,20 +1013,26 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
    if (nt > 0) {
     // one barrier per tile: this wavefront's DMA of tile j has landed (wait), everyone's has and
     // everyone is done reading tile j - 1 (barrier), so its slot takes tile j + PF - 1
+    // tiles j < j_full have no masked key for any row of the wavefront: a loop of its own for them,
+    // so that each loop body holds one variant of the tile arithmetic (with both in one body the
+    // accumulators leave it in other registers than they entered, and are copied back every tile)
     const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
+    const int j_full = min(nt, full_end > c_begin + ks ? (full_end - c_begin - ks + KS - 1) / KS : 0);
     with_niw([&](auto niw_t) {
       constexpr int NIW = decltype(niw_t)::value;
       KVTile<D> cur;
-      for (int j = 0; j < nt; ++j) {
+      auto step = [&](auto masked_t, int j) {
         wait_vm<(PF - 2) * NIW>();
         lds_barrier();
         dma(niw_t, tile(min(j + PF - 1, nt - 1)), (j + PF - 1) % PF);
         if (work) {
           lds_tile(j % PF, cur);
-          if (tile(j) < full_end) compute(std::false_type{}, cur, tile(j));
-          else compute(std::true_type{}, cur, tile(j));
+          compute(masked_t, cur, tile(j));
         }
-      }
+      };
+      int j = 0;
+      for (; j < j_full; ++j) step(std::false_type{}, j);
+      for (; j < nt; ++j) step(std::true_type{}, j);
     });
     wait_vm<0>();   // the ring is empty and read before the next piece refills it
     lds_barrier();
@@ -1218,27 +1229,42 @@ __global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
   // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
   // otherwise pieces 0..S-2 hold l >= 0 and the last piece -2 - l
   const int64_t base = (int64_t)(tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
-  const float enc = lane < a.max_splits ? a.segm_sum[base + lane] : -1.f;
+  // the maxima are fetched with the denominators (one memory round trip), and the pieces' partial
+  // outputs four at a time, so a row costs about three round trips whatever its piece count
+  const bool held = lane < a.max_splits;
+  const float enc = held ? a.segm_sum[base + lane] : -1.f;
+  const float mraw = held ? a.segm_max[base + lane] : -INFINITY;
   const unsigned long long neg = __ballot(enc < 0.f);
   if (neg == 0ull) return;
   const int last = __builtin_ctzll(neg);
   if (last == 0) return;  // not cut
   const int S = last + 1;
   const float ls = lane < last ? enc : (lane == last ? -2.f - enc : 0.f);
-  const float ms = lane < S ? a.segm_max[base + lane] : -INFINITY;
+  const float ms = lane < S ? mraw : -INFINITY;
   const float M = wave_max(ms);
   const float wt = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
   const float den = wave_sum(wt * ls);
   const float inv = 1.f / __builtin_fmaxf(den, 1e-30f);
-  constexpr int CPL = D / WAVE;
+  constexpr int CPL = D / WAVE, UNR = 4;
+  const float* po = a.segm_out + base * D + CPL * lane;
   float num[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) num[e] = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float ws = __shfl(wt, s, WAVE);
-    const float* p = a.segm_out + (base + s) * D + CPL * lane;
+  for (int s0 = 0; s0 < S; s0 += UNR) {
+    float v[UNR][CPL];
 #pragma unroll
-    for (int e = 0; e < CPL; ++e) num[e] = __builtin_fmaf(ws, p[e], num[e]);
+    for (int j = 0; j < UNR; ++j) {  // pieces past the last re-read it (in bounds), unused
+      const float* p = po + (int64_t)min(s0 + j, S - 1) * D;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) v[j][e] = p[e];
+    }
+#pragma unroll
+    for (int j = 0; j < UNR; ++j) {
+      const bool in = s0 + j < S;
+      const float ws = __shfl(wt, min(s0 + j, S - 1), WAVE);
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) num[e] = in ? __builtin_fmaf(ws, v[j][e], num[e]) : num[e];
+    }
   }
   uint16_t* op = a.out + (int64_t)(tok + t) * a.o_st + (int64_t)h * a.o_sh + CPL * lane;
   if constexpr (CPL == 2) {
@@ -1782,6 +1808,22 @@ int resident_blocks(const char* env) {
   return nb;
 }
 
+// wavefronts of kernel k resident per CU at once with `threads` per workgroup and `lds` bytes of
+// dynamic LDS (queried once per shape); DEFAULT_WAVES_PER_CU if the runtime cannot tell
+int resident_waves(const void* k, int threads, size_t lds) {
+  static std::mutex mu;
+  static std::map<std::tuple<const void*, int, size_t>, int> memo;
+  std::lock_guard<std::mutex> guard(mu);
+  const auto key = std::make_tuple(k, threads, lds);
+  const auto it = memo.find(key);
+  if (it != memo.end()) return it->second;
+  int nb = 0;
+  const int w = (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, threads, lds) == hipSuccess && nb > 0)
+                    ? nb * (threads / WAVE) : DEFAULT_WAVES_PER_CU;
+  memo.emplace(key, w);
+  return w;
+}
+
 
 
 }  // namespace
@@ -1975,7 +2017,25 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.min_tiles = MIN_SPLIT_TILES * ks;
   a.seg_cost = seg_cost_units();
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
-  const int64_t tw = target_waves > 0 ? target_waves : (int64_t)device_cus() * DEFAULT_WAVES_PER_CU;
+  // row tiles of the same rows without key splits share each K/V tile through an LDS ring
+  // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
+  a.lds_ring = (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0)) ? 1 : 0;
+  const int pf = a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
+  const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
+                                : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
+  void (*kern)(AttnArgs);
+  if (a.lds_ring) {
+    if (head_dim == 128) kern = pf == 3 ? attn_kernel<128, 3, true> : pf == 6 ? attn_kernel<128, 6, true> : attn_kernel<128, 4, true>;
+    else kern = pf == 3 ? attn_kernel<64, 3, true> : pf == 6 ? attn_kernel<64, 6, true> : attn_kernel<64, 4, true>;
+  } else if (head_dim == 128) {
+    kern = pf == 2 ? attn_kernel<128, 2> : pf == 3 ? attn_kernel<128, 3> : pf == 6 ? attn_kernel<128, 6>
+         : pf == 8 ? attn_kernel<128, 8> : attn_kernel<128, 4>;
+  } else {
+    kern = pf == 2 ? attn_kernel<64, 2> : pf == 3 ? attn_kernel<64, 3> : attn_kernel<64, 4>;
+  }
+  // default grid: as many wavefronts as the chosen kernel keeps resident on the device at once
+  const int64_t tw = target_waves > 0 ? target_waves
+                                      : (int64_t)device_cus() * resident_waves((const void*)kern, WAVE * waves, lds);
   a.workers = (int)std::max<int64_t>(1, std::min<int64_t>(tw / waves, INT32_MAX));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)a.workers);
@@ -1983,33 +2043,7 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   g_ev_start = g_ev_stop = nullptr;
   if (ev0) (void)hipEventRecord(ev0, st);
   const dim3 block(WAVE * waves);
-  // row tiles of the same rows without key splits share each K/V tile through an LDS ring
-  // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
-  a.lds_ring = (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0)) ? 1 : 0;
-  const int pf = a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
-  const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
-                                : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
-  if (a.lds_ring) {
-    if (head_dim == 128) {
-      if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3, true>), grid, block, lds, st, a);
-      else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6, true>), grid, block, lds, st, a);
-      else hipLaunchKernelGGL((attn_kernel<128, 4, true>), grid, block, lds, st, a);
-    } else {
-      if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3, true>), grid, block, lds, st, a);
-      else if (pf == 6) hipLaunchKernelGGL((attn_kernel<64, 6, true>), grid, block, lds, st, a);
-      else hipLaunchKernelGGL((attn_kernel<64, 4, true>), grid, block, lds, st, a);
-    }
-  } else if (head_dim == 128) {
-    if (pf == 2) hipLaunchKernelGGL((attn_kernel<128, 2>), grid, block, lds, st, a);
-    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<128, 3>), grid, block, lds, st, a);
-    else if (pf == 6) hipLaunchKernelGGL((attn_kernel<128, 6>), grid, block, lds, st, a);
-    else if (pf == 8) hipLaunchKernelGGL((attn_kernel<128, 8>), grid, block, lds, st, a);
-    else hipLaunchKernelGGL((attn_kernel<128, 4>), grid, block, lds, st, a);
-  } else {
-    if (pf == 2) hipLaunchKernelGGL((attn_kernel<64, 2>), grid, block, lds, st, a);
-    else if (pf == 3) hipLaunchKernelGGL((attn_kernel<64, 3>), grid, block, lds, st, a);
-    else hipLaunchKernelGGL((attn_kernel<64, 4>), grid, block, lds, st, a);
-  }
+  hipLaunchKernelGGL(kern, grid, block, lds, st, a);
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);
   if (rc != KVQ_OK || num_splits == 1) return rc;

@@ -247,7 +247,7 @@ def choose_splits(max_context, num_seqs=None, num_kv_heads=None, num_q_heads=Non
 
 
 def _target_waves():
-    """Wavefronts the kernel spreads a batch over (KVQ_TARGET_WAVES; 0 = the library's 8 per CU)."""
+    """Wavefronts the kernel spreads a batch over (KVQ_TARGET_WAVES; 0 = as many as the kernel keeps resident)."""
     return int(os.environ.get("KVQ_TARGET_WAVES", "0"))
 
 
