@@ -1217,15 +1217,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 // Merge the pieces of the cut segments (reference kvq/cuda/int8_kv.cu:465-503):
 //   o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30)
-// One wavefront per (request, q head, query token); lane s holds piece s's weight; lanes own D / 64
+// One wavefront per (request, q head, query token), RED_WAVES q heads per workgroup (fewer, larger
+// workgroups: a row is a short chain of dependent loads, and one-wavefront workgroups ran into the
+// per-CU workgroup limit before the wavefront limit); lane s holds piece s's weight; lanes own D / 64
 // channels each. The piece count is read from the denominators (the last piece's is stored as
 // -2 - l, a row that was not cut has -1 in slot 0 and was written by the attention kernel), so the
 // merge needs neither the plan nor any buffer beyond the split buffers of the call.
+constexpr int RED_WAVES = 4;
 template <int D>
-__global__ __launch_bounds__(WAVE) void split_reduce_kernel(AttnArgs a) {
-  const int seq = blockIdx.x, h = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
+__global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int seq = blockIdx.x, t = blockIdx.z;
+  const int h = blockIdx.y * RED_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
-  if (qlen <= 0 || qlen > a.qmax || t >= qlen) return;
+  if (h >= a.G * a.hkv || qlen <= 0 || qlen > a.qmax || t >= qlen) return;
   // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
   // otherwise pieces 0..S-2 hold l >= 0 and the last piece -2 - l
   const int64_t base = (int64_t)(tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
@@ -1999,7 +2004,9 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env))) : DEFAULT_KSPLIT;
   const int ks = std::max(1, std::min(ks_max, MAX_ROW_TILES / rt));
   const int waves = rt * ks;
-  if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535) return fail("int8_decode_attention: grid too large");
+  if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535 || (num_q_heads + RED_WAVES - 1) / RED_WAVES > 65535 ||
+      maxq > 65535)
+    return fail("int8_decode_attention: grid too large");
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = k_cache; a.vc = v_cache; a.out = (uint16_t*)out;
   a.segm_out = segm_out; a.segm_max = segm_max; a.segm_sum = segm_sum;
@@ -2047,9 +2054,9 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);
   if (rc != KVQ_OK || num_splits == 1) return rc;
-  const dim3 rgrid((unsigned)num_seqs, (unsigned)num_q_heads, (unsigned)maxq);
-  if (head_dim == 128) hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE), 0, st, a);
-  else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE), 0, st, a);
+  const dim3 rgrid((unsigned)num_seqs, (unsigned)((num_q_heads + RED_WAVES - 1) / RED_WAVES), (unsigned)maxq);
+  if (head_dim == 128) hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
+  else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
   return launched("split_reduce");
 }
 
