@@ -1470,32 +1470,42 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // Rows past the last key read rows of a valid page; the causal mask drops them. ----
   const int bsm = (1 << a.lbs) - 1;
   uint32_t kvo[IPW], vvo[IPW];   // byte offsets of the lane's chunk from its instruction's first row
+  int64_t kro[IPW], vro[IPW];    // byte offsets of the instruction's first row from its half-tile's first
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
     const int lr = lane / CH, row = RPI * (IPW * wave + i) + lr;
     kvo[i] = (uint32_t)(2 * lr * a.k_sn + 16 * ((lane % CH) ^ kswz(row)));
     vvo[i] = (uint32_t)(2 * lr * a.v_sn + 16 * ((lane % CH) ^ vswz(row)));
+    const int r0 = RPI * (IPW * wave + i) % 16;
+    kro[i] = 2 * r0 * a.k_sn;
+    vro[i] = 2 * r0 * a.v_sn;
   }
   const char* kh = (const char*)(a.kc + (int64_t)kvh * a.k_sh);
   const char* vh = (const char*)(a.vc + (int64_t)kvh * a.v_sh);
+  // tile c: keys 0..15 sit in page p0 from slot (32 c) mod bs on, keys 16..31 right after them
+  // (bs >= 32) or from slot 0 of page p1 (bs == 16); rows past the last key read a valid page
   auto issue = [&](int c, int st) {
     c = min(c, max(ntiles - 1, 0));  // past the end: reload the last tile into the free stage
     const int kb0 = c * PR_KEYS, klast = max(kend - 1, 0);
-    const int i0 = kb0 >> a.lbs, i1 = min(kb0 + PR_KEYS - 1, klast) >> a.lbs;
+    const int i0 = kb0 >> a.lbs, i1 = min(kb0 + 16, klast) >> a.lbs;
     int p0 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i0]);
     int p1 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i1]);
     p0 = (p0 >= 0 && p0 < a.num_blocks) ? p0 : 0;
     p1 = (p1 >= 0 && p1 < a.num_blocks) ? p1 : 0;
+    const int s0 = kb0 & bsm, s1 = (kb0 + 16) & bsm;
+    const char* kb[2] = {kh + 2 * ((int64_t)p0 * a.k_sb + (int64_t)s0 * a.k_sn), kh + 2 * ((int64_t)p1 * a.k_sb + (int64_t)s1 * a.k_sn)};
+    const char* vb[2] = {vh + 2 * ((int64_t)p0 * a.v_sb + (int64_t)s0 * a.v_sn), vh + 2 * ((int64_t)p1 * a.v_sb + (int64_t)s1 * a.v_sn)};
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const int key0 = kb0 + RPI * (IPW * wave + i);
-      const int64_t pg = (key0 >> a.lbs) != i0 ? p1 : p0;
-      const int64_t slot0 = key0 & bsm;
-      const char* kb = kh + 2 * (pg * a.k_sb + slot0 * a.k_sn);   // scalar: the instruction's first row
-      const char* vb = vh + 2 * (pg * a.v_sb + slot0 * a.v_sn);
-      __builtin_amdgcn_global_load_lds((const void*)(kb + (uint64_t)kvo[i]),
+      const int half = RPI * (IPW * wave + i) >= 16;  // uniform
+      // the instruction's first row, kept opaque so that the address stays an SGPR base plus the
+      // lane's 32-bit offset (global_load_lds's saddr form)
+      const char* kr = kb[half] + kro[i];
+      const char* vr = vb[half] + vro[i];
+      asm volatile("" : "+s"(kr), "+s"(vr));
+      __builtin_amdgcn_global_load_lds((const void*)(kr + (uint64_t)kvo[i]),
                                        (__attribute__((address_space(3))) void*)(ring[st][0] + 1024 * (IPW * wave + i)), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(vb + (uint64_t)vvo[i]),
+      __builtin_amdgcn_global_load_lds((const void*)(vr + (uint64_t)vvo[i]),
                                        (__attribute__((address_space(3))) void*)(ring[st][1] + 1024 * (IPW * wave + i)), 16, 0, 0);
     }
   };
@@ -1505,10 +1515,17 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // + 8 (n % 2) of the row (D = 128; D = 64 the same with CH = 8).
   static_assert(CH == 16 || CH == 8, "head_dim 128 or 64");
   const int vr0 = 4 * g + n / 4;
-  uint32_t voff[VT];
+  const uint32_t ring0 = (uint32_t)(uintptr_t)(&ring[0][0][0]);
+  uint32_t vadr[VT];  // stage 0's V^T read addresses; stage st adds st * 2 * TILEB
 #pragma unroll
   for (int tt = 0; tt < VT; ++tt)
-    voff[tt] = vr0 * ROWB + 16 * ((2 * tt + ((n % 4) >> 1)) ^ vswz(vr0)) + 8 * (n & 1);
+    vadr[tt] = ring0 + TILEB + vr0 * ROWB + 16 * ((2 * tt + ((n % 4) >> 1)) ^ vswz(vr0)) + 8 * (n & 1);
+  // stage 0's K operand read addresses of key row n, chunks 4 s + g; row 16 + n has the same swizzle
+  // (row % CH, and CH divides 16), so its reads are the immediate offset 16 * ROWB away
+  static_assert(16 % CH == 0, "rows n and 16 + n share their swizzle");
+  uint32_t kadr[DS];
+#pragma unroll
+  for (int s = 0; s < DS; ++s) kadr[s] = ring0 + n * ROWB + 16 * ((4 * s + g) ^ kswz(n));
 
   float m[RB], l[RB];
   f32x4 acc[RB][VT];
@@ -1528,32 +1545,32 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // stage), which would empty the ring every tile
   auto scores = [&](int st, int c) {
     const int n0 = c * PR_KEYS;
-    const uint32_t kb = (uint32_t)(uintptr_t)(ring[st][0]);
+    const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
+    uint32_t ad[DS];
+#pragma unroll
+    for (int s = 0; s < DS; ++s) ad[s] = kadr[s] + so;
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int row = 16 * b + n;
-      uint32_t ad[DS];
-#pragma unroll
-      for (int s = 0; s < DS; ++s) ad[s] = kb + row * ROWB + 16 * ((4 * s + g) ^ kswz(row));
+      const int KOFS = b * 16 * ROWB;  // key rows 16 + n: same swizzle, 16 rows on
       bf16x8 kop[DS];
       if constexpr (DS == 4) {
         asm volatile(
-            "ds_read_b128 %0, %4\n"
-            "ds_read_b128 %1, %5\n"
-            "ds_read_b128 %2, %6\n"
-            "ds_read_b128 %3, %7\n"
+            "ds_read_b128 %0, %4 offset:%c8\n"
+            "ds_read_b128 %1, %5 offset:%c8\n"
+            "ds_read_b128 %2, %6 offset:%c8\n"
+            "ds_read_b128 %3, %7 offset:%c8\n"
             "s_waitcnt lgkmcnt(0)"
             : "=&v"(kop[0]), "=&v"(kop[1]), "=&v"(kop[2]), "=&v"(kop[3])
-            : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+            : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "i"(KOFS)
             : "memory");
       } else {
         static_assert(DS == 2, "head_dim 128 or 64");
         asm volatile(
-            "ds_read_b128 %0, %2\n"
-            "ds_read_b128 %1, %3\n"
+            "ds_read_b128 %0, %2 offset:%c4\n"
+            "ds_read_b128 %1, %3 offset:%c4\n"
             "s_waitcnt lgkmcnt(0)"
             : "=&v"(kop[0]), "=&v"(kop[1])
-            : "v"(ad[0]), "v"(ad[1])
+            : "v"(ad[0]), "v"(ad[1]), "i"(KOFS)
             : "memory");
       }
 #pragma unroll
@@ -1605,6 +1622,7 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   };
   bool jump = false;  // per lane: a tile's P summed past PR_FAST_PSUM_MAX (only the fast pass reads it)
   auto softmax_pv = [&](int st) {
+    const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
     bf16x8 pop[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -1631,24 +1649,22 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     // transposing reads are issued from inline assembly, 4 channel tiles per statement, each statement
     // waiting for its own reads: the compiler would otherwise make them wait for every LDS DMA in
     // flight (it cannot tell they read another ring stage), emptying the ring each tile.
-    const uint32_t vbase = (uint32_t)(uintptr_t)(ring[st][1]);
     typedef unsigned long long u64;
 #pragma unroll
     for (int t0 = 0; t0 < VT; t0 += 4) {
       u64 lo[4], hi[4];
-      const uint32_t a0 = vbase + voff[t0], a1 = vbase + voff[t0 + 1], a2 = vbase + voff[t0 + 2], a3 = vbase + voff[t0 + 3];
       asm volatile(
-          "ds_read_b64_tr_b16 %0, %8\n"
-          "ds_read_b64_tr_b16 %1, %8 offset:%c12\n"
-          "ds_read_b64_tr_b16 %2, %9\n"
-          "ds_read_b64_tr_b16 %3, %9 offset:%c12\n"
-          "ds_read_b64_tr_b16 %4, %10\n"
-          "ds_read_b64_tr_b16 %5, %10 offset:%c12\n"
-          "ds_read_b64_tr_b16 %6, %11\n"
-          "ds_read_b64_tr_b16 %7, %11 offset:%c12\n"
+          "ds_read_b64_tr_b16 %0, %8 offset:%c12\n"
+          "ds_read_b64_tr_b16 %1, %8 offset:%c13\n"
+          "ds_read_b64_tr_b16 %2, %9 offset:%c12\n"
+          "ds_read_b64_tr_b16 %3, %9 offset:%c13\n"
+          "ds_read_b64_tr_b16 %4, %10 offset:%c12\n"
+          "ds_read_b64_tr_b16 %5, %10 offset:%c13\n"
+          "ds_read_b64_tr_b16 %6, %11 offset:%c12\n"
+          "ds_read_b64_tr_b16 %7, %11 offset:%c13\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]), "=&v"(lo[3]), "=&v"(hi[3])
-          : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "i"(16 * ROWB)
+          : "v"(vadr[t0] + so), "v"(vadr[t0 + 1] + so), "v"(vadr[t0 + 2] + so), "v"(vadr[t0 + 3] + so), "i"(0), "i"(16 * ROWB)
           : "memory");
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -1664,11 +1680,18 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   if (ntiles > 0) {
 #pragma unroll
     for (int j = 0; j < NS - 1; ++j) issue(j, j);
+    // ring stages of tile c (scur) and of the tile DMA'd while c is computed (snext = stage of c - 1),
+    // advanced after each tile (no division in the loop)
+    int scur = 0, snext = NS - 1;
     auto next_tile = [&](int c) {
       wait_vm<2 * IPW * (NS - 2)>();  // this wavefront's share of tile c has landed
       lds_barrier();                  // everyone's share has; stage (c - 1) % NS is free again
-      issue(c + NS - 1, (c + NS - 1) % NS);
-      scores(c % NS, c);
+      issue(c + NS - 1, snext);
+      scores(scur, c);
+    };
+    auto advance = [&]() {
+      scur = scur == NS - 1 ? 0 : scur + 1;
+      snext = snext == NS - 1 ? 0 : snext + 1;
     };
     // Fast pass: tile 0 sets each row's reference maximum (acc is still zero), later tiles only
     // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
@@ -1679,11 +1702,13 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     row_top();
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
-    softmax_pv(0);
+    softmax_pv(scur);
+    advance();
     jump = false;
     for (int c = 1; c < ntiles; ++c) {
       next_tile(c);
-      softmax_pv(c % NS);
+      softmax_pv(scur);
+      advance();
     }
     wait_vm<0>();
     // Rare: a score far above its row's first tile somewhere in the workgroup -- redo the workgroup's
@@ -1699,11 +1724,14 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       }
 #pragma unroll
       for (int j = 0; j < NS - 1; ++j) issue(j, j);
+      scur = 0;
+      snext = NS - 1;
       for (int c = 0; c < ntiles; ++c) {
         next_tile(c);
         row_top();
         if (needs_rescale()) rescale();
-        softmax_pv(c % NS);
+        softmax_pv(scur);
+        advance();
       }
       wait_vm<0>();  // the reloads past the end, before the wavefront exits
     }
