@@ -1389,6 +1389,9 @@ struct PrefillArgs {
   int64_t q_st, q_sh, o_st, o_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, bt_stride;  // elements
   float sm_log2;         // softmax_scale * log2(e)
   int G, lbs, num_blocks;
+  uint32_t kpage, vpage;  // bytes per page (2 k_sb, 2 v_sb: below 2^32)
+  uint32_t krow, vrow;    // bytes per slot (2 k_sn, 2 v_sn: a page's slots span below 2^31 bytes)
+  int contig;             // a page is block_size slots (k_sb = block_size k_sn, v likewise)
 };
 
 constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
@@ -1470,31 +1473,59 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // Rows past the last key read rows of a valid page; the causal mask drops them. ----
   const int bsm = (1 << a.lbs) - 1;
   uint32_t kvo[IPW], vvo[IPW];   // byte offsets of the lane's chunk from its instruction's first row
-  int64_t kro[IPW], vro[IPW];    // byte offsets of the instruction's first row from its half-tile's first
+  uint32_t kro[IPW], vro[IPW];   // byte offsets of the instruction's first row from its half-tile's first
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
     const int lr = lane / CH, row = RPI * (IPW * wave + i) + lr;
     kvo[i] = (uint32_t)(2 * lr * a.k_sn + 16 * ((lane % CH) ^ kswz(row)));
     vvo[i] = (uint32_t)(2 * lr * a.v_sn + 16 * ((lane % CH) ^ vswz(row)));
-    const int r0 = RPI * (IPW * wave + i) % 16;
-    kro[i] = 2 * r0 * a.k_sn;
-    vro[i] = 2 * r0 * a.v_sn;
+    const uint32_t r0 = RPI * (IPW * wave + i) % 16;
+    kro[i] = r0 * a.krow;
+    vro[i] = r0 * a.vrow;
   }
   const char* kh = (const char*)(a.kc + (int64_t)kvh * a.k_sh);
   const char* vh = (const char*)(a.vc + (int64_t)kvh * a.v_sh);
+  // Pages as one run: when the pages the workgroup reads are consecutive ids p_0, p_0 + 1, ... and a
+  // page is bs slots (the layout dequant_pages writes), key k is slot p_0 bs + k of the head's cache:
+  // the tiles' addresses need no block-table read (checked once, by every wavefront alike).
+  bool linear = false;
+  int pfirst = 0;
+  if (ntiles > 0 && a.contig) {
+    const int npg = ((kend - 1) >> a.lbs) + 1;
+    pfirst = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[0]);
+    bool bad = pfirst < 0 || pfirst > a.num_blocks - npg;
+    for (int j = lane; j < npg && !bad; j += WAVE) bad = bt[j] != pfirst + j;
+    linear = !__any(bad);
+  }
+  const char* klin = kh + (uint64_t)(uint32_t)pfirst * a.kpage;
+  const char* vlin = vh + (uint64_t)(uint32_t)pfirst * a.vpage;
   // tile c: keys 0..15 sit in page p0 from slot (32 c) mod bs on, keys 16..31 right after them
   // (bs >= 32) or from slot 0 of page p1 (bs == 16); rows past the last key read a valid page
   auto issue = [&](int c, int st) {
     c = min(c, max(ntiles - 1, 0));  // past the end: reload the last tile into the free stage
     const int kb0 = c * PR_KEYS, klast = max(kend - 1, 0);
-    const int i0 = kb0 >> a.lbs, i1 = min(kb0 + 16, klast) >> a.lbs;
-    int p0 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i0]);
-    int p1 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i1]);
-    p0 = (p0 >= 0 && p0 < a.num_blocks) ? p0 : 0;
-    p1 = (p1 >= 0 && p1 < a.num_blocks) ? p1 : 0;
-    const int s0 = kb0 & bsm, s1 = (kb0 + 16) & bsm;
-    const char* kb[2] = {kh + 2 * ((int64_t)p0 * a.k_sb + (int64_t)s0 * a.k_sn), kh + 2 * ((int64_t)p1 * a.k_sb + (int64_t)s1 * a.k_sn)};
-    const char* vb[2] = {vh + 2 * ((int64_t)p0 * a.v_sb + (int64_t)s0 * a.v_sn), vh + 2 * ((int64_t)p1 * a.v_sb + (int64_t)s1 * a.v_sn)};
+    const char* kb[2];
+    const char* vb[2];
+    if (linear) {
+      // the upper half as below: past the last page (bs == 16) it re-reads the lower half's page
+      const uint32_t k1 = ((min(kb0 + 16, klast) >> a.lbs) << a.lbs) + ((kb0 + 16) & bsm);
+      kb[0] = klin + (uint32_t)kb0 * a.krow;
+      vb[0] = vlin + (uint32_t)kb0 * a.vrow;
+      kb[1] = klin + k1 * a.krow;
+      vb[1] = vlin + k1 * a.vrow;
+    } else {
+      const int i0 = kb0 >> a.lbs, i1 = min(kb0 + 16, klast) >> a.lbs;
+      int p0 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i0]);
+      int p1 = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[i1]);
+      p0 = (p0 >= 0 && p0 < a.num_blocks) ? p0 : 0;
+      p1 = (p1 >= 0 && p1 < a.num_blocks) ? p1 : 0;
+      const uint32_t s0 = kb0 & bsm, s1 = (kb0 + 16) & bsm;
+      // 32 x 32 -> 64-bit page offsets, 32-bit slot offsets
+      kb[0] = kh + ((uint64_t)(uint32_t)p0 * a.kpage + s0 * a.krow);
+      kb[1] = kh + ((uint64_t)(uint32_t)p1 * a.kpage + s1 * a.krow);
+      vb[0] = vh + ((uint64_t)(uint32_t)p0 * a.vpage + s0 * a.vrow);
+      vb[1] = vh + ((uint64_t)(uint32_t)p1 * a.vpage + s1 * a.vrow);
+    }
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const int half = RPI * (IPW * wave + i) >= 16;  // uniform
@@ -1883,6 +1914,9 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 8)
     return fail("paged_prefill_attention: rows must be 16-byte aligned (base pointers and strides)");
   if (rows_per_tile != PR_ROWS) return fail("paged_prefill_attention: work list tiles must be %d rows", PR_ROWS);
+  if (k_sb < 0 || v_sb < 0 || k_sn < 0 || v_sn < 0 || 2 * k_sb > UINT32_MAX || 2 * v_sb > UINT32_MAX ||
+      2 * block_size * k_sn > INT32_MAX || 2 * block_size * v_sn > INT32_MAX)
+    return fail("paged_prefill_attention: page too large for 32-bit page / slot offsets");
   PrefillArgs a;
   a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache; a.out = (uint16_t*)out;
   a.cu_q = cu_seqlens_q; a.seq_lens = seq_lens; a.block_table = block_table; a.tile_req = tile_req; a.tile_row = tile_row;
@@ -1890,6 +1924,9 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
   a.k_sb = k_sb; a.k_sn = k_sn; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sn = v_sn; a.v_sh = v_sh; a.bt_stride = bt_stride;
   a.sm_log2 = (float)(softmax_scale * 1.4426950408889634);
   a.G = (int)(num_q_heads / num_kv_heads); a.lbs = log2i(block_size); a.num_blocks = (int)num_blocks;
+  a.kpage = (uint32_t)(2 * k_sb); a.vpage = (uint32_t)(2 * v_sb);
+  a.krow = (uint32_t)(2 * k_sn); a.vrow = (uint32_t)(2 * v_sn);
+  a.contig = (k_sb == block_size * k_sn && v_sb == block_size * v_sn) ? 1 : 0;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)num_tiles, (unsigned)num_kv_heads);
   if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);

@@ -151,3 +151,51 @@ def test_prefill_score_jump_takes_the_rescaling_pass():
     err = O.compare(torch.stack(list(ref.values())), got)
     record("prefill_score_jump", **err)
     assert torch.isfinite(got).all() and err["max_abs"] <= 2e-2 and err["rel_l2"] < 1e-2, err
+
+
+@pytest.mark.parametrize("layout", ["permuted", "bs32", "bs64_permuted", "padded_pages", "one_page_moved"])
+def test_prefill_page_layouts(layout):
+    """The kernel reads a request's pages without the block table when they are one run of consecutive
+    ids in a cache of whole pages (the layout plan_long + dequant_pages produce), and through the
+    table otherwise: pages in shuffled order, one page of a run moved elsewhere, pages with a stride
+    beyond block_size slots, and larger blocks (one or two pages per 32-key tile). Every layout holds
+    the same logical keys, so each must match the fp32 attention over them."""
+    hq, hkv, d = 12, 2, 128
+    bs = {"bs32": 32, "bs64_permuted": 64}.get(layout, 16)
+    q_lens = [100, 3, 300, 40]
+    seq_lens = [100, 700, 1000, 2000]
+    cu, plan, kt, vt = _temp_cache(q_lens, seq_lens, hkv, d, bs, seed=7)
+    P = kt.shape[0]
+    T = int(cu[-1])
+    q = (torch.randn(T, hq, d, generator=torch.Generator().manual_seed(8)) * 2).to(torch.bfloat16)
+    scale = d ** -0.5
+    ref = _reference(q, kt, vt, cu, seq_lens, plan, scale)       # over the logical pages
+    _, _, bt = plan.gpu(DEV)
+    bt = bt.cpu().long()
+    ktp, vtp = kt, vt
+    if layout in ("permuted", "bs64_permuted", "one_page_moved"):
+        perm = torch.randperm(P + 3, generator=torch.Generator().manual_seed(9))[:P]   # logical -> physical
+        if layout == "one_page_moved":
+            perm = torch.arange(P)
+            perm[P // 2] = P + 2                                  # one page of a run lives elsewhere
+        ktp = torch.zeros(P + 3, bs, hkv, d, dtype=kt.dtype)
+        vtp = torch.zeros_like(ktp)
+        ktp[perm], vtp[perm] = kt, vt
+        bt = torch.where(bt >= 0, perm[bt.clamp(min=0)], bt)
+    elif layout == "padded_pages":                                # page stride of bs + 1 slots
+        ktp = torch.zeros(P, bs + 1, hkv, d, dtype=kt.dtype)
+        vtp = torch.zeros_like(ktp)
+        ktp[:, :bs], vtp[:, :bs] = kt, vt
+    kd, vd = ktp.to(DEV), vtp.to(DEV)
+    if layout == "padded_pages":
+        kd, vd = kd[:, :bs], vd[:, :bs]
+    out = nan_like(q.to(DEV))
+    tile_req, tile_row = plan.tiles(hq // hkv, DEV)
+    ck.ext().paged_prefill_attention(q.to(DEV), kd, vd, out, cu.to(DEV),
+                                     torch.tensor(seq_lens, dtype=torch.int32, device=DEV),
+                                     bt.to(torch.int32).to(DEV), tile_req, tile_row, scale)
+    out = out.cpu()
+    got = torch.stack([out[int(cu[r]) + t] for (r, t) in ref]).float()
+    err = O.compare(torch.stack(list(ref.values())), got)
+    record("prefill_page_layouts", layout=layout, **err)
+    assert torch.isfinite(got).all() and err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3 and err["rel_l2"] < 1e-2, err
