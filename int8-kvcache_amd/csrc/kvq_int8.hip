@@ -649,7 +649,7 @@ constexpr int MERGE_SLOTS = MAX_ROW_TILES - 1;
 #define KVQ_COOP_TILES 8
 #endif
 constexpr int COOP_TILES = KVQ_COOP_TILES;
-constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference maximum     // shortest share of a key split in a split piece, in 32-key tiles
+constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference maximum
 
 // One wavefront's share of one piece of a segment: its 16-row tile (rows row0..row0+15 of the
 // (token, q head) rows of kv head kvh) over the key tiles c_begin + ks, c_begin + ks + KS, ... below
