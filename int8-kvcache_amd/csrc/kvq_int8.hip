@@ -782,74 +782,74 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
                                        16, 0, 0);
     }
   };
-  // this lane's operands of slot st, as load() would put them in registers: K row 16 b + n, logical
-  // chunk (KPL / 16) g + s; V rows 4 g + i (i < 4) and 16 + 4 g + i - 4, bytes VT n .. VT n + VT - 1.
+  // this lane's operands of slot st: K as load() would put them in registers (row 16 b + n, logical
+  // chunk (KPL / 16) g + s), and the V^T operands themselves, read with ds_read_b64_tr_b8: within a
+  // 16-lane group, lane 8 h + b receives byte b of the 8-byte chunks addressed by lanes h, h + 2, ...,
+  // h + 14 (element j from lane h + 2 j). So lane (g, h, j = (lane % 16) / 2) addresses key row
+  // 4 g + j (j < 4) or 16 + 4 g + j - 4 -- the key of P operand slot j of lane group g -- at bytes
+  // 16 t + 8 h, and lane (m = 8 h + b, g) receives channel 16 t + m of its 8 keys: channel tile t is
+  // channels 16 t .. 16 t + 15 here (the register path interleaves them, see the epilogue).
   // Inline assembly, each statement waiting for its own reads: the compiler would otherwise make the
   // reads wait for every DMA in flight (it cannot tell they read another slot).
-  auto lds_tile = [&](int st, KVTile<D>& r) {
-    const uint32_t kb = (uint32_t)(uintptr_t)(lring + st * SLOT), vb = kb + TILE * RB_;
-    uint32_t ka[2][KSTEPS], va[8];
+  uint32_t ka0[2][KSTEPS], vta0[VT];  // slot 0's read addresses
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+  for (int b = 0; b < 2; ++b)
 #pragma unroll
-      for (int s2 = 0; s2 < KSTEPS; ++s2) {
-        const int row = 16 * b + n;
-        ka[b][s2] = kb + row * RB_ + 16 * (((KPL / 16) * g + s2) ^ (row % CHR));
-      }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = i < 4 ? 4 * g + i : 16 + 4 * g + i - 4;
-      const int byte = VT * n;
-      va[i] = vb + row * RB_ + 16 * ((byte / 16) ^ (row % CHR)) + byte % 16;
+    for (int s2 = 0; s2 < KSTEPS; ++s2) {
+      const int row = 16 * b + n;
+      ka0[b][s2] = (uint32_t)(uintptr_t)lring + row * RB_ + 16 * (((KPL / 16) * g + s2) ^ (row % CHR));
     }
+  {
+    const int j = (lane & 15) >> 1, h = lane & 1;
+    const int row = j < 4 ? 4 * g + j : 16 + 4 * g + j - 4;
+#pragma unroll
+    for (int t = 0; t < VT; ++t)
+      vta0[t] = (uint32_t)(uintptr_t)lring + TILE * RB_ + row * RB_ + 16 * (t ^ (row % CHR)) + 8 * h;
+  }
+  auto lds_tile = [&](int st, KVTile<D>& r) {
+    const uint32_t so = (uint32_t)(st * SLOT);
+    typedef unsigned long long u64;
+    u64 w[VT];
     if constexpr (D == 128) {
-      typedef unsigned long long u64;
-      u64 w[8];
       asm volatile(
           "ds_read_b128 %0, %12\n"
           "ds_read_b128 %1, %13\n"
           "ds_read_b128 %2, %14\n"
           "ds_read_b128 %3, %15\n"
-          "ds_read_b64 %4, %16\n"
-          "ds_read_b64 %5, %17\n"
-          "ds_read_b64 %6, %18\n"
-          "ds_read_b64 %7, %19\n"
-          "ds_read_b64 %8, %20\n"
-          "ds_read_b64 %9, %21\n"
-          "ds_read_b64 %10, %22\n"
-          "ds_read_b64 %11, %23\n"
+          "ds_read_b64_tr_b8 %4, %16\n"
+          "ds_read_b64_tr_b8 %5, %17\n"
+          "ds_read_b64_tr_b8 %6, %18\n"
+          "ds_read_b64_tr_b8 %7, %19\n"
+          "ds_read_b64_tr_b8 %8, %20\n"
+          "ds_read_b64_tr_b8 %9, %21\n"
+          "ds_read_b64_tr_b8 %10, %22\n"
+          "ds_read_b64_tr_b8 %11, %23\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(r.k[0][0]), "=&v"(r.k[0][1]), "=&v"(r.k[1][0]), "=&v"(r.k[1][1]), "=&v"(w[0]), "=&v"(w[1]),
             "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
-          : "v"(ka[0][0]), "v"(ka[0][1]), "v"(ka[1][0]), "v"(ka[1][1]), "v"(va[0]), "v"(va[1]), "v"(va[2]),
-            "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7])
+          : "v"(ka0[0][0] + so), "v"(ka0[0][1] + so), "v"(ka0[1][0] + so), "v"(ka0[1][1] + so), "v"(vta0[0] + so),
+            "v"(vta0[1] + so), "v"(vta0[2] + so), "v"(vta0[3] + so), "v"(vta0[4] + so), "v"(vta0[5] + so),
+            "v"(vta0[6] + so), "v"(vta0[7] + so)
           : "memory");
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        r.v[i][0] = (uint32_t)w[i];
-        r.v[i][1] = (uint32_t)(w[i] >> 32);
-      }
     } else {
-      uint32_t w[8];
       asm volatile(
-          "ds_read_b128 %0, %10\n"
-          "ds_read_b128 %1, %11\n"
-          "ds_read_b32 %2, %12\n"
-          "ds_read_b32 %3, %13\n"
-          "ds_read_b32 %4, %14\n"
-          "ds_read_b32 %5, %15\n"
-          "ds_read_b32 %6, %16\n"
-          "ds_read_b32 %7, %17\n"
-          "ds_read_b32 %8, %18\n"
-          "ds_read_b32 %9, %19\n"
+          "ds_read_b128 %0, %6\n"
+          "ds_read_b128 %1, %7\n"
+          "ds_read_b64_tr_b8 %2, %8\n"
+          "ds_read_b64_tr_b8 %3, %9\n"
+          "ds_read_b64_tr_b8 %4, %10\n"
+          "ds_read_b64_tr_b8 %5, %11\n"
           "s_waitcnt lgkmcnt(0)"
-          : "=&v"(r.k[0][0]), "=&v"(r.k[1][0]), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]),
-            "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
-          : "v"(ka[0][0]), "v"(ka[1][0]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]),
-            "v"(va[6]), "v"(va[7])
+          : "=&v"(r.k[0][0]), "=&v"(r.k[1][0]), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+          : "v"(ka0[0][0] + so), "v"(ka0[1][0] + so), "v"(vta0[0] + so), "v"(vta0[1] + so), "v"(vta0[2] + so),
+            "v"(vta0[3] + so)
           : "memory");
+    }
+    // the V^T operand of channel tile t, two dwords per tile, in r.v's storage
 #pragma unroll
-      for (int i = 0; i < 8; ++i) r.v[i][0] = w[i];
+    for (int t = 0; t < VT; ++t) {
+      r.v[(2 * t) / VW][(2 * t) % VW] = (uint32_t)w[t];
+      r.v[(2 * t + 1) / VW][(2 * t + 1) % VW] = (uint32_t)(w[t] >> 32);
     }
   };
   const int niw = (NI + a.rt - 1) / a.rt;    // DMA instructions per wavefront and tile (uniform)
@@ -929,9 +929,13 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
       for (int s = 0; s < KSTEPS; ++s) z = __builtin_amdgcn_mfma_i32_16x16x64_i8(r.k[b][s], qop[s], z, 0, 0, 0);
       sc[b] = z;
     }
-    // ---- V^T operands: 8x8 byte transpose per channel tile ----
+    // ---- V^T operands: 8x8 byte transpose per channel tile (the LDS ring reads them transposed) ----
     long vop[VT];
-    if constexpr (VW == 2) {
+    if constexpr (SHARED) {
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+        vop[t] = (long)(((uint64_t)r.v[(2 * t + 1) / VW][(2 * t + 1) % VW] << 32) | r.v[(2 * t) / VW][(2 * t) % VW]);
+    } else if constexpr (VW == 2) {
       static_assert(VT == 8, "head_dim 128: two V dwords per lane and key, 8 channel tiles");
       uint32_t lo[8], hi[8];  // lo[t] = keys j 0..3 of channel tile t, hi[t] = keys j 4..7
       transpose4x4(r.v[0][0], r.v[1][0], r.v[2][0], r.v[3][0], lo[0], lo[1], lo[2], lo[3]);
@@ -1059,7 +1063,8 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     }
   }
 
-  // ---- epilogue: lane (n, g) holds channels (D/4) g + (D/16) i + t of row n ----
+  // ---- epilogue: lane (n, g) holds channels (D/4) g + (D/16) i + t of row n in acc[t][i] (register
+  // path), or channels 16 t + 4 g + i (LDS ring path) ----
   l = group4_sum(l);
   if (KS > 1) {
     // key-split merge (the formula of split_reduce_kernel): wavefronts k >= 1 publish (m, l, acc),
@@ -1103,6 +1108,36 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   constexpr int OPL = D / 4;
   const int head = kvh * G + rh;
   const int qt = tok + rtok;
+  if constexpr (SHARED) {
+    float vsc[VT][4];
+#pragma unroll
+    for (int t = 0; t < VT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vsc[t][i] = a.vs_pc ? a.vs[kvh * D + 16 * t + 4 * g + i] : a.vs[kvh];
+    if (nparts == 1) {
+      if (a.max_splits > 1 && g == 0)
+        a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
+      const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
+      uint16_t* orow = a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + 4 * g;
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+        *reinterpret_cast<u32x2*>(orow + 16 * t) =
+            u32x2{pack_bf16x2((acc[t][0] * inv) * vsc[t][0], (acc[t][1] * inv) * vsc[t][1]),
+                  pack_bf16x2((acc[t][2] * inv) * vsc[t][2], (acc[t][3] * inv) * vsc[t][3])};
+    } else {
+      const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + part;
+      if (g == 0) {
+        a.segm_max[sidx] = m;
+        a.segm_sum[sidx] = part == nparts - 1 ? -2.f - l : l;
+      }
+      float* sp = a.segm_out + sidx * D + 4 * g;
+#pragma unroll
+      for (int t = 0; t < VT; ++t)
+        *reinterpret_cast<float4*>(sp + 16 * t) =
+            float4{acc[t][0] * vsc[t][0], acc[t][1] * vsc[t][1], acc[t][2] * vsc[t][2], acc[t][3] * vsc[t][3]};
+    }
+    return;
+  }
   float vsc[OPL];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
