@@ -1536,12 +1536,17 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   const char* vlin = vh + (uint64_t)(uint32_t)pfirst * a.vpage;
   // tile c: keys 0..15 sit in page p0 from slot (32 c) mod bs on, keys 16..31 right after them
   // (bs >= 32) or from slot 0 of page p1 (bs == 16); rows past the last key read a valid page
-  auto issue = [&](int c, int st) {
+  // lin_t: std::true_type = the pages are one run (no block-table read), false_type = read the
+  // table, bool = decide at run time
+  auto issue = [&](int c, int st, auto lin_t) {
     c = min(c, max(ntiles - 1, 0));  // past the end: reload the last tile into the free stage
     const int kb0 = c * PR_KEYS, klast = max(kend - 1, 0);
     const char* kb[2];
     const char* vb[2];
-    if (linear) {
+    bool lin;
+    if constexpr (std::is_same_v<decltype(lin_t), bool>) lin = lin_t;
+    else lin = decltype(lin_t)::value;
+    if (lin) {
       // the upper half as below: past the last page (bs == 16) it re-reads the lower half's page
       const uint32_t k1 = ((min(kb0 + 16, klast) >> a.lbs) << a.lbs) + ((kb0 + 16) & bsm);
       kb[0] = klin + (uint32_t)kb0 * a.krow;
@@ -1609,7 +1614,9 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // K operand reads from inline assembly, each statement waiting for its own reads: as plain loads
   // the compiler makes them wait for every LDS DMA in flight (it cannot tell they read another ring
   // stage), which would empty the ring every tile
-  auto scores = [&](int st, int c) {
+  // mask_t: std::false_type = no key of the tile is past any row's limit; true_type = test when the
+  // tile reaches the causal edge of some row of the wavefront
+  auto scores = [&](int st, int c, auto mask_t) {
     const int n0 = c * PR_KEYS;
     const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
     uint32_t ad[DS];
@@ -1646,7 +1653,7 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
           sc[rb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[s], qop[rb][s], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : sc[rb][b],
                                                              0, 0, 0);
     }
-    if (n0 + PR_KEYS > lim_lo) {  // a tile on the causal edge of some row of the wavefront
+    if (decltype(mask_t)::value && n0 + PR_KEYS > lim_lo) {  // a tile on the causal edge of some row
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -1745,15 +1752,15 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
 
   if (ntiles > 0) {
 #pragma unroll
-    for (int j = 0; j < NS - 1; ++j) issue(j, j);
+    for (int j = 0; j < NS - 1; ++j) issue(j, j, linear);
     // ring stages of tile c (scur) and of the tile DMA'd while c is computed (snext = stage of c - 1),
     // advanced after each tile (no division in the loop)
     int scur = 0, snext = NS - 1;
-    auto next_tile = [&](int c) {
+    auto next_tile = [&](int c, auto lin_t, auto mask_t) {
       wait_vm<2 * IPW * (NS - 2)>();  // this wavefront's share of tile c has landed
       lds_barrier();                  // everyone's share has; stage (c - 1) % NS is free again
-      issue(c + NS - 1, snext);
-      scores(scur, c);
+      issue(c + NS - 1, snext, lin_t);
+      scores(scur, c, mask_t);
     };
     auto advance = [&]() {
       scur = scur == NS - 1 ? 0 : scur + 1;
@@ -1763,19 +1770,31 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
     // exceeds the reference by more than 60 (log2 units); a lane whose P sum says one did is only
     // flagged (in softmax_pv) -- acc is never changed under a condition, which keeps the accumulators
-    // in place in registers.
-    next_tile(0);
-    row_top();
+    // in place in registers. The tiles below J have no key past any row's limit; with the page
+    // addressing fixed per loop, their loop body is one block of straight-line code.
+    const int J = min(ntiles, max(lim_lo, 0) / PR_KEYS);
+    auto fast_pass = [&](auto lin_t) {
+      next_tile(0, lin_t, std::true_type{});
+      row_top();
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
-    softmax_pv(scur);
-    advance();
-    jump = false;
-    for (int c = 1; c < ntiles; ++c) {
-      next_tile(c);
+      for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
       softmax_pv(scur);
       advance();
-    }
+      jump = false;
+      int c = 1;
+      for (; c < J; ++c) {
+        next_tile(c, lin_t, std::false_type{});
+        softmax_pv(scur);
+        advance();
+      }
+      for (; c < ntiles; ++c) {
+        next_tile(c, lin_t, std::true_type{});
+        softmax_pv(scur);
+        advance();
+      }
+    };
+    if (linear) fast_pass(std::true_type{});
+    else fast_pass(std::false_type{});
     wait_vm<0>();
     // Rare: a score far above its row's first tile somewhere in the workgroup -- redo the workgroup's
     // tiles with a reference maximum raised (and acc / l rescaled) whenever a score exceeds it by
@@ -1789,11 +1808,11 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
         for (int tt = 0; tt < VT; ++tt) acc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
 #pragma unroll
-      for (int j = 0; j < NS - 1; ++j) issue(j, j);
+      for (int j = 0; j < NS - 1; ++j) issue(j, j, linear);
       scur = 0;
       snext = NS - 1;
       for (int c = 0; c < ntiles; ++c) {
-        next_tile(c);
+        next_tile(c, linear, std::true_type{});
         row_top();
         if (needs_rescale()) rescale();
         softmax_pv(scur);
