@@ -521,3 +521,50 @@ def test_key_split_workgroups_agree(q_len, segm):
     record("ksplit_vs_plain", q_len=q_len, segm=segm, **e)
     assert torch.isfinite(split.float()).all() and e["rel_l2"] < 1e-3 and e["max_abs"] <= 1e-2, e
     check_attention(oracle_attention(c, kq, vq), split, "ksplit_vs_oracle", q_len=q_len)
+
+
+# ------------------------------------------------------------------ block sizes beyond 16
+@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("H,D", [(4, 128), (2, 64), (3, 128)])
+def test_quant_cache_block_sizes(bs, H, D):
+    """Cache blocks of 32 and 64 slots (vLLM's other block sizes), interleaved layout; both kernels
+    (H x D a multiple of 512 or not); codes bit-exact."""
+    r = synth.rng(bs * 100 + H * 10 + D)
+    T, nb = 500, 24
+    key = synth.bf16(r.standard_normal((T, H, D)) * 4)
+    value = synth.bf16(r.standard_normal((T, H, D)))
+    slots = torch.from_numpy(r.permutation(nb * bs)[:T].astype(np.int64))
+    slots[::11] = -1
+    st = synth.scales_from(key, value, per_channel=True)
+    kv = torch.zeros(nb, H, bs, 2 * D, dtype=torch.int8)
+    kc, vc = kv.transpose(1, 2).split(D, dim=-1)
+    O.quant_cache_ref(key, value, kc, vc, slots, st)
+    kv_d = torch.zeros_like(kv, device=DEV)
+    kc_d, vc_d = kv_d.transpose(1, 2).split(D, dim=-1)
+    ck.quant_reshape_and_cache(dev(key), dev(value), kc_d, vc_d, dev(slots), dev(st))
+    assert torch.equal(kv_d.cpu(), kv)
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+@pytest.mark.parametrize("shape", [(28, 4, 128), (14, 2, 64), (32, 8, 128)])
+@pytest.mark.parametrize("case", ["decode", "short"])
+def test_attention_block_sizes(bs, shape, case):
+    """Decode rows (the register-ring kernel) and up-to-8-token causal queries (the LDS-ring kernel
+    when a (request, kv head) has more than 32 rows) over caches of 32- and 64-slot blocks, with and
+    without split buffers: against the oracle at the attention bar."""
+    hq, hkv, d = shape
+    q_lens, seq_lens = CASES[case]
+    c = synth.paged_case(hq, hkv, q_lens, seq_lens, head_dim=d, block_size=bs, seed=bs + hq + d, dist="randn",
+                         scale=3.0)
+    c["static"] = synth.scales_from(c["k"].reshape(-1, hkv, d), c["v"].reshape(-1, hkv, d), True)
+    c["scale"] = d ** -0.5
+    kq, vq = int8_cache(c)
+    ref = oracle_attention(c, kq, vq, True)
+    ref64 = oracle_attention(c, kq, vq, True, q_arith="fp64")
+    dc = dev(c)
+    T = c["q"].shape[0]
+    for segm in (None, nan_segm(T, hq, 8, d)):
+        out = ck.decode_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
+                                  dc["block_table"], c["scale"], dc["static"], segm=segm,
+                                  max_query_len=max(q_lens))
+        check_attention(ref, out, "block_sizes", ref_fp64=ref64, heads=list(shape), case=case, bs=bs)
