@@ -806,43 +806,51 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     for (int t = 0; t < VT; ++t)
       vta0[t] = (uint32_t)(uintptr_t)lring + TILE * RB_ + row * RB_ + 16 * (t ^ (row % CHR)) + 8 * h;
   }
-  auto lds_tile = [&](int st, KVTile<D>& r) {
-    const uint32_t so = (uint32_t)(st * SLOT);
+  // st_t: the slot, an int or a std::integral_constant (then its offset is the reads' immediate)
+  auto lds_tile = [&](auto st_t, KVTile<D>& r) {
+    constexpr bool CT = !std::is_same_v<decltype(st_t), int>;
+    uint32_t so;
+    if constexpr (CT) so = 0;
+    else so = (uint32_t)(st_t * SLOT);
+    constexpr int IMM = [] {
+      if constexpr (CT) return decltype(st_t)::value * SLOT;
+      else return 0;
+    }();
     typedef unsigned long long u64;
     u64 w[VT];
     if constexpr (D == 128) {
       asm volatile(
-          "ds_read_b128 %0, %12\n"
-          "ds_read_b128 %1, %13\n"
-          "ds_read_b128 %2, %14\n"
-          "ds_read_b128 %3, %15\n"
-          "ds_read_b64_tr_b8 %4, %16\n"
-          "ds_read_b64_tr_b8 %5, %17\n"
-          "ds_read_b64_tr_b8 %6, %18\n"
-          "ds_read_b64_tr_b8 %7, %19\n"
-          "ds_read_b64_tr_b8 %8, %20\n"
-          "ds_read_b64_tr_b8 %9, %21\n"
-          "ds_read_b64_tr_b8 %10, %22\n"
-          "ds_read_b64_tr_b8 %11, %23\n"
+          "ds_read_b128 %0, %12 offset:%c24\n"
+          "ds_read_b128 %1, %13 offset:%c24\n"
+          "ds_read_b128 %2, %14 offset:%c24\n"
+          "ds_read_b128 %3, %15 offset:%c24\n"
+          "ds_read_b64_tr_b8 %4, %16 offset:%c24\n"
+          "ds_read_b64_tr_b8 %5, %17 offset:%c24\n"
+          "ds_read_b64_tr_b8 %6, %18 offset:%c24\n"
+          "ds_read_b64_tr_b8 %7, %19 offset:%c24\n"
+          "ds_read_b64_tr_b8 %8, %20 offset:%c24\n"
+          "ds_read_b64_tr_b8 %9, %21 offset:%c24\n"
+          "ds_read_b64_tr_b8 %10, %22 offset:%c24\n"
+          "ds_read_b64_tr_b8 %11, %23 offset:%c24\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(r.k[0][0]), "=&v"(r.k[0][1]), "=&v"(r.k[1][0]), "=&v"(r.k[1][1]), "=&v"(w[0]), "=&v"(w[1]),
             "=&v"(w[2]), "=&v"(w[3]), "=&v"(w[4]), "=&v"(w[5]), "=&v"(w[6]), "=&v"(w[7])
           : "v"(ka0[0][0] + so), "v"(ka0[0][1] + so), "v"(ka0[1][0] + so), "v"(ka0[1][1] + so), "v"(vta0[0] + so),
             "v"(vta0[1] + so), "v"(vta0[2] + so), "v"(vta0[3] + so), "v"(vta0[4] + so), "v"(vta0[5] + so),
-            "v"(vta0[6] + so), "v"(vta0[7] + so)
+            "v"(vta0[6] + so), "v"(vta0[7] + so), "i"(IMM)
           : "memory");
     } else {
       asm volatile(
-          "ds_read_b128 %0, %6\n"
-          "ds_read_b128 %1, %7\n"
-          "ds_read_b64_tr_b8 %2, %8\n"
-          "ds_read_b64_tr_b8 %3, %9\n"
-          "ds_read_b64_tr_b8 %4, %10\n"
-          "ds_read_b64_tr_b8 %5, %11\n"
+          "ds_read_b128 %0, %6 offset:%c12\n"
+          "ds_read_b128 %1, %7 offset:%c12\n"
+          "ds_read_b64_tr_b8 %2, %8 offset:%c12\n"
+          "ds_read_b64_tr_b8 %3, %9 offset:%c12\n"
+          "ds_read_b64_tr_b8 %4, %10 offset:%c12\n"
+          "ds_read_b64_tr_b8 %5, %11 offset:%c12\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(r.k[0][0]), "=&v"(r.k[1][0]), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
           : "v"(ka0[0][0] + so), "v"(ka0[1][0] + so), "v"(vta0[0] + so), "v"(vta0[1] + so), "v"(vta0[2] + so),
-            "v"(vta0[3] + so)
+            "v"(vta0[3] + so), "i"(IMM)
           : "memory");
     }
     // the V^T operand of channel tile t, two dwords per tile, in r.v's storage
@@ -1025,18 +1033,36 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     with_niw([&](auto niw_t) {
       constexpr int NIW = decltype(niw_t)::value;
       KVTile<D> cur;
-      auto step = [&](auto masked_t, int j) {
+      // tile j sits in slot st = j % PF and its DMA goes to slot (j + PF - 1) % PF: ints, or
+      // compile-time constants in the rounds below (the reads' slot offset is then an immediate)
+      auto step = [&](auto masked_t, int j, auto st, auto dst) {
         wait_vm<(PF - 2) * NIW>();
         lds_barrier();
-        dma(niw_t, tile(min(j + PF - 1, nt - 1)), (j + PF - 1) % PF);
+        dma(niw_t, tile(min(j + PF - 1, nt - 1)), (int)dst);
         if (work) {
-          lds_tile(j % PF, cur);
+          lds_tile(st, cur);
           compute(masked_t, cur, tile(j));
         }
       };
       int j = 0;
-      for (; j < j_full; ++j) step(std::false_type{}, j);
-      for (; j < nt; ++j) step(std::true_type{}, j);
+      // whole rounds of PF unmasked tiles (a round starts at a multiple of PF: slots 0 .. PF - 1)
+      for (; j + PF <= j_full; j += PF) {
+        auto round_step = [&](auto jj_t) {
+          constexpr int JJ = decltype(jj_t)::value;
+          if constexpr (JJ < PF)
+            step(std::false_type{}, j + JJ, std::integral_constant<int, JJ>{},
+                 std::integral_constant<int, (JJ + PF - 1) % PF>{});
+        };
+        round_step(std::integral_constant<int, 0>{});
+        round_step(std::integral_constant<int, 1>{});
+        round_step(std::integral_constant<int, 2>{});
+        round_step(std::integral_constant<int, 3>{});
+        round_step(std::integral_constant<int, 4>{});
+        round_step(std::integral_constant<int, 5>{});
+        static_assert(PF <= 6, "rounds are written for up to 6 slots");
+      }
+      for (; j < j_full; ++j) step(std::false_type{}, j, j % PF, (j + PF - 1) % PF);
+      for (; j < nt; ++j) step(std::true_type{}, j, j % PF, (j + PF - 1) % PF);
     });
     wait_vm<0>();   // the ring is empty and read before the next piece refills it
     lds_barrier();
