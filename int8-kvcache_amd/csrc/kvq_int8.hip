@@ -54,6 +54,8 @@ constexpr int DEFAULT_KSPLIT = 2;     // key splits per row tile: skewed batches
 constexpr int DEFAULT_LDS_PREFETCH = 3;   // shared LDS ring slots (3, 4 and 6 time the same on c3)
 constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: skewed batches (c4's
                                       // lengths; 10 x 32k + 86 x 1 keys) time best at 6-16
+constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kernel (4 row tiles filling
+                                               // one ring): verification batches time best at 12
 constexpr int DEFAULT_PREFETCH = 3;
 constexpr int NUM_XCDS = 8;
 
@@ -1901,13 +1903,14 @@ int log2i(int64_t x) {
 // instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
 // Work units (32-key tiles of one workgroup's streaming) charged per segment for its fixed cost in
 // the stream-K partition (KVQ_SEG_COST overrides)
-int seg_cost_units() {
-  static const int c = [] {
+int seg_cost_units(bool lds_ring) {
+  static const int env = [] {
     const char* e = getenv("KVQ_SEG_COST");
-    const int v = e ? atoi(e) : DEFAULT_SEG_COST;
+    if (!e) return -1;
+    const int v = atoi(e);
     return v < 0 ? 0 : (v > 64 ? 64 : v);
   }();
-  return c;
+  return env >= 0 ? env : (lds_ring ? DEFAULT_SEG_COST_LDS_RING : DEFAULT_SEG_COST);
 }
 
 // slots of the attention's shared LDS ring (KVQ_LDS_PREFETCH: 3, 4 or 6)
@@ -2167,11 +2170,11 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
   a.max_splits = (int)num_splits; a.rt = rt; a.ksplit = ks; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES * ks;
-  a.seg_cost = seg_cost_units();
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
   a.lds_ring = (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0)) ? 1 : 0;
+  a.seg_cost = seg_cost_units(a.lds_ring != 0);
   const int pf = a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
   const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
                                 : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
