@@ -1899,10 +1899,8 @@ int log2i(int64_t x) {
   while ((int64_t(1) << r) < x) ++r;
   return r;
 }
-// Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
-// instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
 // Work units (32-key tiles of one workgroup's streaming) charged per segment for its fixed cost in
-// the stream-K partition (KVQ_SEG_COST overrides)
+// the stream-K partition, per kernel (KVQ_SEG_COST overrides both)
 int seg_cost_units(bool lds_ring) {
   static const int env = [] {
     const char* e = getenv("KVQ_SEG_COST");
@@ -1923,6 +1921,8 @@ int lds_prefetch_depth() {
   return depth;
 }
 
+// Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
+// instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
 int prefetch_depth() {
   static const int depth = [] {
     const char* e = getenv("KVQ_PREFETCH");
