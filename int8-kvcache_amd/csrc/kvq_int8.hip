@@ -1461,7 +1461,7 @@ constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
 constexpr int PR_ROWS = 4 * 16 * PR_RB;     // rows per workgroup (4 wavefronts)
 constexpr int PR_KEYS = 32;                 // keys per tile
 constexpr float PR_SLACK = 8.f;             // log2 headroom of the reference maximum (general loop)
-constexpr float PR_FAST_PSUM_MAX = 0x1p60f;  // largest per-lane P sum the fast pass takes (P <= 2^60)
+constexpr float PR_FAST_PSUM_MAX = 0x1p60f;  // largest per-lane denominator the fast pass takes (P <= 2^60)
 constexpr int PR_STAGES = 3;                // LDS ring: tiles in flight + the one computed (3 x 16 KB: 3 workgroups per CU)
 
 // two floats -> two bf16 (round to nearest even, v_cvt_pk_bf16_f32)
@@ -1721,7 +1721,6 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
     }
   };
-  bool jump = false;  // per lane: a tile's P summed past PR_FAST_PSUM_MAX (only the fast pass reads it)
   auto softmax_pv = [&](int st) {
     const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
     bf16x8 pop[RB];
@@ -1735,9 +1734,6 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
           p[b][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[rb][b][i], a.sm_log2, -m[rb]));
           psum += p[b][i];
         }
-      // unflagged, every P of the lane is <= 2^60 (far from any fp32 / bf16 overflow in P, l or acc);
-      // a score more than 60 above the reference (log2 units) makes its P, hence the sum, exceed it
-      jump |= !(psum <= PR_FAST_PSUM_MAX);
       l[rb] += psum;
       u32x4 pw;
       pw.x = pack_bf16x2_rne(p[0][0], p[0][1]);
@@ -1796,10 +1792,12 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     };
     // Fast pass: tile 0 sets each row's reference maximum (acc is still zero), later tiles only
     // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
-    // exceeds the reference by more than 60 (log2 units); a lane whose P sum says one did is only
-    // flagged (in softmax_pv) -- acc is never changed under a condition, which keeps the accumulators
-    // in place in registers. The tiles below J have no key past any row's limit; with the page
-    // addressing fixed per loop, their loop body is one block of straight-line code.
+    // exceeds the reference by more than 60 (log2 units). Every P is at most its lane's denominator
+    // l (a sum of P >= 0), so a lane whose l ends at most 2^60 (and not NaN) saw no such score;
+    // any other lane sends the workgroup to the general pass below -- acc is never changed under a
+    // condition, which keeps the accumulators in place in registers. The tiles below J have no key
+    // past any row's limit; with the page addressing fixed per loop, their loop body is one block
+    // of straight-line code.
     const int J = min(ntiles, max(lim_lo, 0) / PR_KEYS);
     auto fast_pass = [&](auto lin_t) {
       next_tile(0, lin_t, std::true_type{});
@@ -1808,7 +1806,6 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       for (int rb = 0; rb < RB; ++rb) m[rb] = __builtin_fmaxf(top[rb], -1e30f);
       softmax_pv(scur);
       advance();
-      jump = false;
       int c = 1;
       for (; c < J; ++c) {
         next_tile(c, lin_t, std::false_type{});
@@ -1824,6 +1821,9 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     if (linear) fast_pass(std::true_type{});
     else fast_pass(std::false_type{});
     wait_vm<0>();
+    bool jump = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) jump |= !(l[rb] <= PR_FAST_PSUM_MAX);
     // Rare: a score far above its row's first tile somewhere in the workgroup -- redo the workgroup's
     // tiles with a reference maximum raised (and acc / l rescaled) whenever a score exceeds it by
     // 2^PR_SLACK.
