@@ -568,3 +568,38 @@ def test_attention_block_sizes(bs, shape, case):
                                   dc["block_table"], c["scale"], dc["static"], segm=segm,
                                   max_query_len=max(q_lens))
         check_attention(ref, out, "block_sizes", ref_fp64=ref64, heads=list(shape), case=case, bs=bs)
+
+
+def test_attention_events_hook_times_one_call():
+    """kvq_set_attention_events (no counterpart in the reference; bench.py's timing hook): the next
+    decode_attention call records the pair around its attention kernel on its stream and forgets it,
+    so a later call records nothing into the same events; the output is unaffected."""
+    import ctypes
+    from kvq import _native
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventQuery.argtypes = [ctypes.c_void_p]
+    ev = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for e in ev:
+        assert hip.hipEventCreate(ctypes.byref(e)) == 0
+    try:
+        c = synth.paged_case(28, 4, [1] * 6, [300, 1000, 4000, 17, 2047, 64], seed=5, dist="randn", scale=3.0)
+        c["static"] = synth.scales_from(c["k"].reshape(-1, 4, 128), c["v"].reshape(-1, 4, 128), True)
+        kq, vq = int8_cache(c)
+        dc = dev(c)
+        lib = _native.load()
+        assert lib.kvq_set_attention_events(ev[0], ev[1]) == 0
+        out1 = ck.decode_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
+                                   dc["block_table"], 128 ** -0.5, dc["static"])
+        torch.cuda.synchronize()
+        ms = ctypes.c_float()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0 and ms.value > 0
+        first = ms.value
+        out2 = ck.decode_attention(dc["q"], dev(kq), dev(vq), nan_like(dc["q"]), dc["cu"], dc["seq_lens"],
+                                   dc["block_table"], 128 ** -0.5, dc["static"])
+        torch.cuda.synchronize()
+        assert hip.hipEventElapsedTime(ctypes.byref(ms), ev[0], ev[1]) == 0 and ms.value == first  # not re-recorded
+        assert torch.equal(out1, out2)
+    finally:
+        for e in ev:
+            hip.hipEventDestroy(e)
