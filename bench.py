@@ -114,6 +114,30 @@ def time_c2(w, steps, warmup):
     return out, (t1 - t0) * 1e3 / steps, statistics.mean(kern_ms), statistics.median(kern_ms), splits
 
 
+def read_ceiling(buf, reps=10):
+    """GB/s a plain streaming read of `buf` sustains on this device (the library's kvq_stream_read):
+    what HBM delivers to a read-only stream, the ceiling beside the attention kernel's rate."""
+    nbytes = buf.numel() * buf.element_size() // 16 * 16
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream().cuda_stream
+    best = (0.0, 0)
+    for per_cu in (4, 8):   # the better of two grid sizes
+        wg = cus * per_cu
+        out = torch.empty(wg * 256, dtype=torch.int32, device=DEV)
+        for _ in range(2):
+            _native.call("kvq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), wg, stream)
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            _native.call("kvq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), wg, stream)
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        best = max(best, (nbytes / (statistics.median(ts) * 1e-3) / 1e9, per_cu))
+    return best
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
     """The CPU oracle (port of int8_ref B + run_paged) on whole c2 requests until ~budget_s of CPU work;
@@ -406,6 +430,12 @@ def main():
                      "kernel": "attn_kernel<128,3>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
+    ceil_gbs, ceil_wg = read_ceiling(w["kv"])
+    res["roofline"]["read_ceiling"] = {
+        "GBps": round(ceil_gbs, 1), "frac_of_peak": round(ceil_gbs / PEAK_GBS, 4),
+        "kernel_frac_of_ceiling": round(res["roofline"]["achieved"] / ceil_gbs, 4),
+        "how": "kvq_stream_read over the c2 cache's %d bytes (contiguous share per workgroup, 8 loads in flight per lane, "
+               "%d workgroups of 256 lanes per CU, the better of 4 and 8), HIP events, median of 10" % (w["kv"].numel(), ceil_wg)}
     prof = os.path.join(REPO, "profiles", "attn_kernel_c2_traffic.json")
     if os.path.exists(prof):   # HBM bytes per launch from the committed rocprofv3 --pmc runs of this workload
         with open(prof) as f:

@@ -129,6 +129,13 @@ int kvq_prefill_rows_per_tile(void);
  * benchmark time the attention kernel alone with events. Returns 0. */
 int kvq_set_attention_events(void* start, void* stop);
 
+/* Instrumentation, no counterpart in the reference: reads `bytes` bytes at `data` (16-byte aligned, a
+ * multiple of 16) once with `workgroups` workgroups of 256 lanes (each streaming a contiguous share,
+ * non-temporal loads) and writes each lane's XOR of the 32-bit words it read to out[workgroups * 256]. Timing it gives the
+ * streaming-read rate HBM sustains on the device, the ceiling bench.py reports beside the attention
+ * kernel. Stream-ordered, allocates nothing. */
+int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t workgroups, void* stream);
+
 /* Text of the last error on this thread ("" if none). */
 const char* kvq_last_error(void);
 

@@ -1867,6 +1867,37 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Streaming-read probe (instrumentation, no counterpart in the reference): reads n16 16-byte words
+// once and stores each lane's XOR of what it read (so no load is dropped). Workgroup b streams the
+// b-th contiguous share of the buffer, its wavefronts taking interleaved 1 KB blocks of it with 8
+// non-temporal loads in flight per lane -- the way the attention kernel streams its pages. What it
+// sustains is what HBM delivers to a read-only stream on the box at hand: the ceiling the decode
+// attention kernel is compared with.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                          uint32_t* __restrict__ out) {
+  constexpr int DEPTH = 8;
+  const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+  const int64_t share = (n16 + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = min((int64_t)blockIdx.x * share, n16), hi = min(lo + share, n16);
+  uint32_t acc = 0;
+  int64_t i = lo + (int64_t)wave * WAVE + lane;
+  constexpr int64_t STEP = 4 * WAVE;  // the 4 wavefronts' interleaved 1 KB blocks
+  for (; i + (DEPTH - 1) * STEP < hi; i += DEPTH * STEP) {
+    u32x4 v[DEPTH];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) v[d] = __builtin_nontemporal_load(p + i + d * STEP);
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) acc ^= v[d].x ^ v[d].y ^ v[d].z ^ v[d].w;
+  }
+  for (; i < hi; i += STEP) {
+    const u32x4 a = __builtin_nontemporal_load(p + i);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  out[(int64_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+// ------------------------------------------------------------------------------------------------
 // Host side: argument checks, launches, error reporting.
 // ------------------------------------------------------------------------------------------------
 thread_local std::string g_err;
@@ -2023,7 +2054,15 @@ int kvq_set_attention_events(void* start, void* stop) {
   return KVQ_OK;
 }
 
-int kvq_abi_version(void) { return 3; }
+int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t workgroups, void* stream) {
+  if (!data || !out || bytes < 16 || bytes % 16 || !aligned16(data) || workgroups < 1 || workgroups > INT32_MAX / 256)
+    return fail("stream_read: need a 16-byte aligned buffer of a positive multiple of 16 bytes and 1..2^23 workgroups");
+  hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)workgroups), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const u32x4*>(data), bytes / 16, out);
+  return launched("stream_read");
+}
+
+int kvq_abi_version(void) { return 4; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 

@@ -603,3 +603,18 @@ def test_attention_events_hook_times_one_call():
     finally:
         for e in ev:
             hip.hipEventDestroy(e)
+
+
+@pytest.mark.parametrize("nbytes,wg", [(1 << 20, 64), ((1 << 20) + 48, 7), (16, 1), (5 * 4096 + 16, 2048)])
+def test_stream_read_probe_reads_every_word_once(nbytes, wg):
+    """kvq_stream_read (bench.py's read-ceiling probe, no counterpart in the reference): the XOR of the
+    lanes' outputs is the XOR of every 32-bit word of the buffer, whatever the grid."""
+    from kvq import _native
+    g = torch.Generator().manual_seed(nbytes + wg)
+    host = torch.randint(-2 ** 31, 2 ** 31 - 1, (nbytes // 4,), generator=g, dtype=torch.int32)
+    buf = host.to(DEV)
+    out = torch.full((wg * 256,), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+    _native.call("kvq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), wg, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
+    assert got == np.bitwise_xor.reduce(host.numpy().view(np.uint32))
