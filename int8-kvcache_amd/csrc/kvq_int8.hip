@@ -370,8 +370,12 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
     tab[t][i % (CH / 4)] = v;
   }
   __syncthreads();
-  if (t_first >= n) return;
-  const int steps = (n - 1 - t_first) / stride + 1;   // tokens of this wavefront: t_first + k * stride
+  // tokens of this wavefront: tpw consecutive ones from t0, so that each workgroup streams a
+  // contiguous run of key / value rows (the interleaved order -- token t_first + k * stride -- timed
+  // 0.7% slower on c1)
+  const int tpw = (n + stride - 1) / stride, t0 = t_first * tpw;
+  if (t0 >= n) return;
+  const int steps = min(tpw, n - t0);
   const int64_t bmask = (int64_t(1) << lbs) - 1;
   // per-lane byte offsets within a token's rows (all extents < 2^31 bytes: host)
   const int koff = 2 * (h * key_sh + d0), voff = 2 * (h * val_sh + d0);
@@ -382,7 +386,7 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
   u32x4 kin[QC_ROW_PF], vin[QC_ROW_PF];
   // fetches are issued in ring order (scheduling barriers: the waits count on that order)
   auto fetch = [&](int j, int k) {  // k clamped: past the end it re-reads the wavefront's last token
-    const int t = t_first + min(k, steps - 1) * stride;
+    const int t = t0 + min(k, steps - 1);
     slot[j] = slots[t];
     __builtin_amdgcn_sched_barrier(0);
     kin[j] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, 2 * t * key_st, QC_LOAD_AUX);

@@ -618,3 +618,20 @@ def test_stream_read_probe_reads_every_word_once(nbytes, wg):
     torch.cuda.synchronize()
     got = np.bitwise_xor.reduce(out.cpu().numpy().view(np.uint32))
     assert got == np.bitwise_xor.reduce(host.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("wg_per_cu", ["1", "2"])
+def test_quant_cache_ring_path_bit_exact(monkeypatch, wg_per_cu):
+    """The wavefront-row kernel's token ring (more tokens per wavefront than it keeps in flight at
+    once), forced by a small grid (KVQ_QC_WG_PER_CU): c1's full input, codes bit-exact."""
+    monkeypatch.setenv("KVQ_QC_WG_PER_CU", wg_per_cu)
+    c = synth.c1_inputs()
+    nb, bs = c["num_blocks"], c["block_size"]
+    n = c["slots"].shape[0] - 5                          # not a multiple of the wavefront count
+    kv = torch.zeros(nb, 4, bs, 256, dtype=torch.int8)
+    kc, vc = kv.transpose(1, 2).split(128, dim=-1)
+    O.quant_cache_ref(c["key"], c["value"], kc, vc, c["slots"][:n], c["static"])
+    kv_d = torch.zeros_like(kv, device=DEV)
+    kc_d, vc_d = kv_d.transpose(1, 2).split(128, dim=-1)
+    ck.quant_reshape_and_cache(dev(c["key"]), dev(c["value"]), kc_d, vc_d, dev(c["slots"][:n]), dev(c["static"]))
+    assert torch.equal(kv_d.cpu(), kv)
