@@ -1347,10 +1347,10 @@ __global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs
 }
 
 // ------------------------------------------------------------------------------------------------
-// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542). Blocks walk
-// the output pages with a grid stride; a lane converts 16 channels of one (token, head): a 16-byte
-// int8 load, two 16-byte bf16 stores (v_cvt_pk_bf16_f32, round to nearest even). When the lanes of
-// a token divide the block, each lane keeps its (head, channels) and their scales for the launch.
+// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542). One wavefront
+// per (output page, head), the 4 wavefronts of a workgroup on consecutive heads of one page (so a
+// workgroup reads and writes contiguous runs); a lane converts 16 channels of one (token, head): a
+// 16-byte int8 load, two 16-byte bf16 stores (v_cvt_pk_bf16_f32, round to nearest even).
 // ------------------------------------------------------------------------------------------------
 __device__ __forceinline__ float i8f(uint32_t w, int b) { return (float)(int8_t)(w >> (8 * b)); }
 
