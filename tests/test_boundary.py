@@ -67,6 +67,24 @@ def test_native_call_raises_with_message():
                      None, 3, None, 96, None, 96, None)
 
 
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    # no fallback: without the built library, the ops API raises instead of computing anything
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(_native, "LIB_PATH", str(tmp_path / "libkvq_int8.so"))
+    monkeypatch.setattr(ck, "_EXT", None)
+    with pytest.raises(_native.NativeError, match="is not built"):
+        ck.ext()
+    with pytest.raises(_native.NativeError, match="is not built"):
+        _native.call("kvq_abi_version")
+
+
+def test_wrong_abi_version_fails_loudly(monkeypatch):
+    monkeypatch.setattr(_native, "_LIB", None)
+    monkeypatch.setattr(_native, "ABI_VERSION", _native.ABI_VERSION + 1000)
+    with pytest.raises(_native.NativeError, match="rebuild it"):
+        _native.load()
+
+
 # ------------------------------------------------------------ Python API: the reference's TORCH_CHECKs
 def test_python_api_shape_checks():
     q = torch.zeros(3, 28, 64, dtype=torch.bfloat16)
