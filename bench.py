@@ -384,7 +384,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this path has no multi-GPU mode (every kernel shards per request / "
-              "kv head with no exchange; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "kv head with no exchange, so each GPU would run this same workload on its share). "
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     torch.cuda.set_device(0)
     if args.copy_calibration:
