@@ -5,7 +5,8 @@ Headline (BASELINE.json metric, config c2): INT8 paged decode attention, 128 req
 28 q / 4 kv heads, head_dim 128, block 16, in vLLM's interleaved [nb, H, bs, 2D] int8 cache (filled
 with c0-distribution codes by this package's quantize-and-cache kernel), shuffled block tables over
 263,168 blocks. A step is one kvq.cuda_kernels.decode_attention call (attention kernel + split merge)
-with every input resident in HBM.
+with split buffers allocated once beforehand, as the vLLM backend passes its metadata's, and every input
+resident in HBM. The same call without split buffers (one pass, nothing allocated) is reported beside it.
 
 Prints ONE JSON line. `value` is algorithmic bytes / step time (GB/s); `roofline` times the attention
 kernel alone with HIP events recorded around it on its own stream; `cpu_baseline` times the CPU oracle
@@ -89,12 +90,17 @@ def build_c2(B=128, L=32768, hq=28, hkv=4, d=128, bs=16):
             "hq": hq, "hkv": hkv, "d": d, "bs": bs, "alg_bytes": alg, "kv_bytes": B * L * hkv * d * 2}
 
 
-def time_c2(w, steps, warmup):
+def time_c2(w, steps, warmup, split=True):
+    """Step time and attention-kernel time of c2. split: the call carries split buffers allocated once
+    beforehand (as the vLLM backend passes its metadata's softmax_segm_* buffers), sized for the table
+    width by choose_splits; otherwise the one-pass call without them (nothing cut, nothing allocated)."""
     out = torch.empty_like(w["q"])
     scale = w["d"] ** -0.5
+    splits = ck.choose_splits(w["bt"].shape[1] * w["bs"]) if split else 1
+    segm = ck.split_buffers(w["B"], w["hq"], w["d"], splits, DEV) if split else None
 
     def step():
-        ck.decode_attention(w["q"], w["kc"], w["vc"], out, w["cu"], w["sl"], w["bt"], scale, w["st"])
+        ck.decode_attention(w["q"], w["kc"], w["vc"], out, w["cu"], w["sl"], w["bt"], scale, w["st"], segm=segm)
 
     for _ in range(warmup):
         step()
@@ -110,7 +116,6 @@ def time_c2(w, steps, warmup):
     t1 = time.perf_counter()
     kern_ms = [ev.elapsed_ms(i) for i in range(steps)]
     ev.close()
-    splits = ck.choose_splits(w["bt"].shape[1] * w["bs"])
     return out, (t1 - t0) * 1e3 / steps, statistics.mean(kern_ms), statistics.median(kern_ms), splits
 
 
@@ -285,7 +290,7 @@ def bench_c1(reps=20):
             "alg_bytes": alg, "tokens": T, "valid": t_valid}
 
 
-def bench_c3(reps=20):
+def bench_c3(reps=20, one_pass=True):
     """64 requests x 8 query tokens (causal), L log-uniform in [512, 8192], 28/4/128: two cache copies
     (~360 MB) rotated."""
     lens = synth.c3_lens()
@@ -304,20 +309,23 @@ def bench_c3(reps=20):
     cu = torch.arange(65, dtype=torch.int32, device=DEV) * 8
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
+    segm = ck.split_buffers(q.shape[0], hq, d, ck.choose_splits(sets[0][2].shape[1] * bs), DEV)
 
-    def fn(i):
+    def fn(i, segm=segm):
         kc, vc, bt = sets[i]
-        ck.decode_attention(q, kc, vc, out, cu, sl, bt, d ** -0.5, st, max_query_len=8)
+        ck.decode_attention(q, kc, vc, out, cu, sl, bt, d ** -0.5, st, segm=segm, max_query_len=8)
 
     ms = _median_event_ms(fn, reps, len(sets))
+    ms1 = _median_event_ms(lambda i: fn(i, None), reps, len(sets)) if one_pass else float("nan")
     kvb = sum(lens) * hkv * d * 2
     alg = kvb + 2 * q.numel() * 2 + sum(pages) * 4 + 129 * 4 + 2 * hkv * d * 4
     ops = sum(lens) * hkv * 28672
     return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
-            "alg_bytes": alg, "useful_int8_ops": ops, "mfma_util": round(ops / (ms * 1e-3) / PEAK_INT8_OPS, 5)}
+            "alg_bytes": alg, "useful_int8_ops": ops, "mfma_util": round(ops / (ms * 1e-3) / PEAK_INT8_OPS, 5),
+            "one_pass_us": round(ms1 * 1e3, 2)}
 
 
-def bench_c4(reps=10):
+def bench_c4(reps=10, one_pass=True):
     """Llama-3 heads (32 / 8, d128): 96 decode rows (L log-uniform in [1, 32768]) through the INT8
     kernel, and the 4 x 16384-token prefill requests' pages dequantized to bf16 (dequant_pages)."""
     lens = synth.c4_lens()
@@ -336,7 +344,11 @@ def bench_c4(reps=10):
     cu = torch.arange(97, dtype=torch.int32, device=DEV)
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
-    ms_dec = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st), reps, 1)
+    segm = ck.split_buffers(96, hq, d, ck.choose_splits(bt.shape[1] * bs), DEV)
+    ms_dec = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st, segm=segm),
+                              reps, 1)
+    ms_dec1 = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st), reps,
+                               1) if one_pass else float("nan")
     cu_all = torch.tensor([0] + [int(x) for x in torch.cumsum(torch.tensor([1] * 96 + pre), 0)], dtype=torch.int32)
     plan = ck.plan_long(cu_all, torch.tensor(lens + pre), bs)
     src_req, src_j, _ = plan.gpu(DEV)
@@ -362,7 +374,7 @@ def bench_c4(reps=10):
     dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
     dq_alg = P * bs * hkv * d * 2 * (1 + 2) + P * 12
     return {"decode_us": round(ms_dec * 1e3, 2), "decode_GBps": round(dec_alg / ms_dec / 1e6, 1),
-            "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4),
+            "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4), "decode_one_pass_us": round(ms_dec1 * 1e3, 2),
             "dequant_us": round(ms_dq * 1e3, 2), "dequant_GBps": round(dq_alg / ms_dq / 1e6, 1),
             "dequant_frac": round(dq_alg / ms_dq / 1e6 / PEAK_GBS, 4), "dequant_pages": P,
             "prefill_ms": round(ms_pf, 3), "prefill_TFLOPs": round(pf_flop / ms_pf / 1e9, 1),
@@ -404,7 +416,9 @@ def main():
         bad = [x for x in names if x not in runs]
         if bad:
             ap.error("unknown extras %s (choose from c1, c3, c4)" % bad)
-        print(json.dumps({"extra": {runs[x][0]: runs[x][1]() for x in names}}), flush=True)
+        # profiling runs: only the calls with split buffers (the one-pass variants launch the same kernel)
+        kw = lambda x: {} if x == "c1" else {"one_pass": False}
+        print(json.dumps({"extra": {runs[x][0]: runs[x][1](**kw(x)) for x in names}}), flush=True)
         return
     print("# building c2 workload", file=sys.stderr, flush=True)
     w = build_c2()
@@ -431,6 +445,13 @@ def main():
                      "kernel": "attn_kernel<128,3>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
+    _, ms1, k1_mean, _, _ = time_c2(w, max(5, args.steps // 2), 2, split=False)
+    res["c2_one_pass"] = {"what": "the same call without split buffers: one pass, each (request, kv head) whole in "
+                                  "one workgroup, nothing allocated (what the vLLM backend runs when num_reqs > "
+                                  "seq_threshold_3D)",
+                          "us_per_call": round(ms1 * 1e3, 1), "kernel_us_mean": round(k1_mean * 1e3, 1),
+                          "GBps": round(alg / (ms1 * 1e-3) / 1e9, 1),
+                          "frac": round(alg / (ms1 * 1e-3) / 1e9 / PEAK_GBS, 4)}
     ceil_gbs, ceil_wg = read_ceiling(w["kv"])
     res["roofline"]["read_ceiling"] = {
         "GBps": round(ceil_gbs, 1), "frac_of_peak": round(ceil_gbs / PEAK_GBS, 4),

@@ -76,8 +76,11 @@ int kvq_quant_q(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens, i
  * segm_out [T, Hq, S, D] and segm_max / segm_sum [T, Hq, S] (element (t, h, s) at
  * t * seg_st + h * seg_sh + s, segm_out at that index * D + d), which a second kernel merges.
  * num_splits (<= 64) is S, the most pieces the buffers hold: no segment is cut into more.
- * num_splits == 1: nothing is cut (segm_* may be NULL). The split buffers are scratch of the call:
- * their contents are internal (segm_sum carries the piece count in its sign), as the reference's. */
+ * num_splits == 1 (the reference's single pass without split buffers, int8_kv.cu:612-613): nothing
+ * is cut and segm_* may be NULL -- each (request, kv head, row group) runs whole in the workgroup
+ * whose range it starts in, its keys split over the workgroup's wavefronts and merged in LDS; one
+ * kernel, no second launch. The split buffers are scratch of the call: their contents are internal
+ * (segm_sum carries the piece count in its sign), as the reference's. */
 int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
                               int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
                               int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,

@@ -531,10 +531,10 @@ __device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
 }
 // Length, in work units, of each of the request's (kv head, row group) segments: seg_cost units for
 // its fixed cost (q load and quantization, the block-table walk's first round trips, the finish and
-// output write -- latency a one-tile segment pays as much as a long one), then one unit per tile; or
-// 1 when segments are never cut (no split buffers).
+// output write -- latency a one-tile segment pays as much as a long one), then one unit per tile.
+// Without split buffers segments are never cut, but the same lengths still balance the workers.
 __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
-  return a.max_splits == 1 ? (w.ntiles ? 1 : 0) : (w.ntiles ? a.seg_cost + w.ntiles : 0);
+  return w.ntiles ? a.seg_cost + w.ntiles : 0;
 }
 
 // The batch as one line of work units: request by request, kv head by kv head, row group by row
@@ -542,6 +542,8 @@ __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
 // same amount of work -- K/V to stream plus the segments' fixed costs -- however skewed the request
 // lengths are. chunk is also long enough that no segment is cut into more than max_splits pieces.
 // The merge kernel needs none of it: it reads each segment's piece count from the denominators.
+// Without split buffers (max_splits 1) a workgroup instead runs, whole, every segment that starts
+// inside its range.
 struct Plan {
   long long total, chunk;
 };
@@ -1249,12 +1251,15 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     const int take = (int)min((long long)(seglen - off), end - pos);
     // the segment's first seg_cost units stand for its fixed cost, the rest for its tiles: pieces are
     // the workers' shares of the tile units (a worker holding only fixed-cost units has no piece, and
-    // the pieces are numbered from the worker holding the first tile)
-    const int fc = whole ? 0 : a.seg_cost;
-    const long long first = (seg_start + fc) / pl.chunk, last = (seg_start + seglen - 1) / pl.chunk;
+    // the pieces are numbered from the worker holding the first tile). Uncut (whole): the worker where
+    // the segment starts runs all of it, one piece.
+    const int fc = a.seg_cost;
+    const long long first = whole ? worker : (seg_start + fc) / pl.chunk;
+    const long long last = whole ? worker : (seg_start + seglen - 1) / pl.chunk;
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
     const int row0 = (rg * a.rt + rtile) * 16;
-    const int c0 = whole ? 0 : max(off - fc, 0), c1 = whole ? w.ntiles : max(off + take - fc, 0);
+    const int c0 = whole ? 0 : max(off - fc, 0);
+    const int c1 = whole ? (off == 0 ? w.ntiles : 0) : max(off + take - fc, 0);
     // a piece long enough for every key split to stream COOP_TILES tiles is split across them and
     // merged; shorter pieces go whole to one key split in turn (no barrier, no merge)
     if (c1 <= c0) {
@@ -1292,12 +1297,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // merge needs neither the plan nor any buffer beyond the split buffers of the call.
 constexpr int RED_WAVES = 4;
 template <int D>
-__global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs a) {
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int seq = blockIdx.x, t = blockIdx.z;
-  const int h = blockIdx.y * RED_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
-  if (h >= a.G * a.hkv || qlen <= 0 || qlen > a.qmax || t >= qlen) return;
+__device__ __forceinline__ void merge_row(const AttnArgs& a, int tok, int t, int h, int lane) {
   // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
   // otherwise pieces 0..S-2 hold l >= 0 and the last piece -2 - l
   const int64_t base = (int64_t)(tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
@@ -1344,6 +1344,17 @@ __global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs
   } else {
     op[0] = (uint16_t)bf16_rne(num[0] * inv);
   }
+}
+// Grid (request, group of RED_WAVES q heads, z): block z merges query tokens z, z + gridDim.z, ... of
+// its request, so every short request's rows are covered whatever max_query_len the caller reported.
+template <int D>
+__global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int seq = blockIdx.x;
+  const int h = blockIdx.y * RED_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
+  if (h >= a.G * a.hkv || qlen <= 0 || qlen > a.qmax) return;
+  for (int t = blockIdx.z; t < qlen; t += gridDim.z) merge_row<D>(a, tok, t, h, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2006,7 +2017,14 @@ int resident_waves(const void* k, int threads, size_t lds) {
   return w;
 }
 
-
+int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb, int64_t k_sn,
+                     int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn, int64_t v_sh, int64_t num_blocks,
+                     int64_t block_size, int64_t num_kv_heads, int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
+                     float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
+                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
 
 }  // namespace
 
@@ -2170,6 +2188,24 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               int64_t v_scale_cols, double softmax_scale, float* segm_out, float* segm_max,
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
                               int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream) {
+  return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
+                          num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
+                          num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
+                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb, int64_t k_sn,
+                     int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn, int64_t v_sh, int64_t num_blocks,
+                     int64_t block_size, int64_t num_kv_heads, int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
+                     float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
+                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("int8_decode_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("int8_decode_attention: block_size must be a power of two >= 16");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -2192,7 +2228,10 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   // key splits fill up to DEFAULT_KSPLIT wavefronts per row tile, within the workgroup's 4
   // (KVQ_KSPLIT overrides, 1: none)
   const char* ks_env = getenv("KVQ_KSPLIT");
-  const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env))) : DEFAULT_KSPLIT;
+  // Without split buffers nothing is cut across workgroups: as many key splits as the workgroup
+  // holds then run each segment
+  const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env)))
+                            : (num_splits == 1 ? MAX_ROW_TILES : DEFAULT_KSPLIT);
   const int ks = std::max(1, std::min(ks_max, MAX_ROW_TILES / rt));
   const int waves = rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535 || (num_q_heads + RED_WAVES - 1) / RED_WAVES > 65535 ||
@@ -2250,6 +2289,10 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
   return launched("split_reduce");
 }
+
+}  // namespace
+
+extern "C" {
 
 int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t k_sh, const int8_t* v_cache,
                       int64_t v_sb, int64_t v_sn, int64_t v_sh, int64_t num_blocks, int64_t block_size,

@@ -234,16 +234,24 @@ def quant_q(q, k_scale, group=None):
 MIN_SPLIT_KEYS = 128   # the kernels never cut a split shorter than 4 tiles of 32 keys
 
 
-def choose_splits(max_context, num_seqs=None, num_kv_heads=None, num_q_heads=None, max_query_len=1, num_cus=None):
-    """Most splits per request for a batch whose caller passes no split buffers (the kernel then uses,
-    per request, only as many as its length and the batch's total work call for -- see
-    include/kvq_int8.h): enough for the longest possible context (block-table width x block size)
-    to be cut into ranges of 128 keys, at most 64. KVQ_SPLITS overrides it (1 = never split). A pure
-    function of host-side shapes, so a captured graph and the eager call agree."""
+def choose_splits(max_context):
+    """Split buffers' piece count for a caller that sizes them from shapes alone (bench.py, tests): enough
+    for the longest possible context (block-table width x block size) to be cut into ranges of 128 keys,
+    at most 64. KVQ_SPLITS overrides it (1 = never split). A pure function of host-side shapes, so a
+    captured graph and the eager call agree."""
     env = os.environ.get("KVQ_SPLITS")
     if env:
         return max(1, min(MAX_SPLITS, int(env)))
     return int(max(1, min(MAX_SPLITS, -(-max(max_context, 1) // MIN_SPLIT_KEYS))))
+
+
+def split_buffers(num_tokens, num_q_heads, head_dim, splits, device):
+    """(segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) float32: the split buffers
+    decode_attention / paged_attention take as `segm` (what vLLM's Triton metadata holds as
+    softmax_segm_output / _max / _expsum)."""
+    return (torch.empty(num_tokens, num_q_heads, splits, head_dim, dtype=torch.float32, device=device),
+            torch.empty(num_tokens, num_q_heads, splits, dtype=torch.float32, device=device),
+            torch.empty(num_tokens, num_q_heads, splits, dtype=torch.float32, device=device))
 
 
 def _target_waves():
@@ -256,17 +264,10 @@ def decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_tab
     """INT8 attention for the requests with at most SHORT_Q query tokens (others are skipped).
     max_query_len bounds the short queries' length (reference kvq/cuda_kernels.py:51-58).
 
-    segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) allows up to S splits per
-    request (the reference always uses S); the kernel gives each request as many of them as its share
-    of the batch's work calls for. Without segm the cap comes from the shapes (choose_splits) and the
-    partial buffers from torch's allocator."""
-    if segm is None and cu_seqlens_q.shape[0] > 1:
-        S = choose_splits(block_table.shape[1] * k_cache.shape[1])
-        if S > 1:
-            T, Hq, D = q.shape
-            segm = (torch.empty(T, Hq, S, D, dtype=torch.float32, device=q.device),
-                    torch.empty(T, Hq, S, dtype=torch.float32, device=q.device),
-                    torch.empty(T, Hq, S, dtype=torch.float32, device=q.device))
+    segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) allows up to S pieces per
+    (request, kv head) (the reference always uses S); the kernel gives each as many of them as its share
+    of the batch's work calls for. Without segm nothing is cut and nothing is allocated: one pass, each
+    (request, kv head) whole in one workgroup (the reference's S = 1, kvq/cuda/int8_kv.cu:612-613)."""
     so, sm, ss = segm if segm is not None else (None, None, None)
     ext().int8_decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, static["k_scale"],
                                 static["v_scale"], softmax_scale, so, sm, ss, max_query_len, SHORT_Q)

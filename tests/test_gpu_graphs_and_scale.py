@@ -131,7 +131,7 @@ def _interleaved(nb, hkv, bs, d):
 def test_c2_full_size_sampled_parity():
     """c2: 128 requests x 32768 keys in vLLM's interleaved cache, filled through the quantize-and-cache
     kernel. Checks: the fill's codes for a sample of blocks are bit-exact; 6 sampled requests match the
-    oracle; the output does not depend on the split count (KVQ_SPLITS 1 vs the default)."""
+    oracle with split buffers (bench.py's step); the output without them (one pass, nothing cut) agrees."""
     B, L, hq, hkv, d, bs = 128, 32768, 28, 4, 128, 16
     pages = L // bs
     nb = B * pages + 64
@@ -149,25 +149,23 @@ def test_c2_full_size_sampled_parity():
     q = torch.randn(B, hq, d, generator=g, device=DEV).to(torch.bfloat16)
     cu = torch.arange(B + 1, dtype=torch.int32, device=DEV)
     sl = torch.full((B,), L, dtype=torch.int32, device=DEV)
-    out = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st)
+    out = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st,
+                              segm=nan_segm(B, hq, ck.choose_splits(bt.shape[1] * bs), d))
     for r in (0, 17, 63, 64, 100, 127):
         ref = _request_oracle(kc, vc, bt, r, L, q[r:r + 1], st)
         err = O.compare(ref, out[r:r + 1].cpu())
         record("c2_sampled", request=r, **err)
         assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (r, err)
-    os.environ["KVQ_SPLITS"] = "1"
-    try:
-        one = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st)
-    finally:
-        del os.environ["KVQ_SPLITS"]
+    one = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st)
     e = O.compare(one.cpu(), out.cpu())
     record("c2_split_invariance", **e)
     assert e["rel_l2"] < 1e-3 and e["max_abs"] <= 1e-2
 
 
-def test_c3_verification_full_parity():
+@pytest.mark.parametrize("split", [True, False])
+def test_c3_verification_full_parity(split):
     """c3: 64 requests x 8 causal query tokens, L log-uniform in [512, 8192]: every request against
-    the oracle."""
+    the oracle, with split buffers (bench.py's call) and without (one pass)."""
     lens = synth.c3_lens()
     c = synth.paged_case(28, 4, [8] * 64, lens, seed=13, params=synth.channel_params(4, 128), pool=1)
     c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
@@ -177,16 +175,19 @@ def test_c3_verification_full_parity():
     ref = O.paged_static_attention(O.CFG32_Q32, st, True, 8)(c["q"].float(), kq, vq, c["cu"], c["seq_lens"],
                                                                c["block_table"], SCALE)
     d = {k: v.to(DEV) for k, v in c.items() if isinstance(v, torch.Tensor)}
+    segm = nan_segm(d["q"].shape[0], 28, ck.choose_splits(d["block_table"].shape[1] * 16), 128) if split else None
     out = ck.decode_attention(d["q"], kq.to(DEV), vq.to(DEV), nan_like(d["q"]), d["cu"], d["seq_lens"],
-                              d["block_table"], SCALE, {k: v.to(DEV) for k, v in st.items()}, max_query_len=8)
+                              d["block_table"], SCALE, {k: v.to(DEV) for k, v in st.items()}, segm=segm,
+                              max_query_len=8)
     err = O.compare(ref, out.cpu())
-    record("c3_full", **err)
+    record("c3_full", split=split, **err)
     assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3 and err["rel_l2"] < 5e-3, err
 
 
-def test_c4_decode_rows_sampled_parity():
+@pytest.mark.parametrize("split", [True, False])
+def test_c4_decode_rows_sampled_parity(split):
     """c4 decode part: Llama-3 heads (32 / 8), 96 requests with L log-uniform in [1, 32768] (incl. 1,
-    17 and 32768): 12 requests against the oracle."""
+    17 and 32768): 12 requests against the oracle, with split buffers and without."""
     lens = synth.c4_lens()
     hq, hkv, d, bs = 32, 8, 128, 16
     pages = [-(-L // bs) for L in lens]
@@ -199,11 +200,12 @@ def test_c4_decode_rows_sampled_parity():
     g = torch.Generator(device=DEV).manual_seed(7)
     q = torch.randn(96, hq, d, generator=g, device=DEV).to(torch.bfloat16)
     cu = torch.arange(97, dtype=torch.int32, device=DEV)
+    segm = nan_segm(96, hq, ck.choose_splits(bt.shape[1] * bs), d) if split else None
     out = ck.decode_attention(q, kc, vc, nan_like(q), cu, torch.tensor(lens, dtype=torch.int32, device=DEV),
-                              bt, SCALE, st)
+                              bt, SCALE, st, segm=segm)
     order = sorted(range(96), key=lambda r: lens[r])
     for r in [0, 1, 2] + order[::10]:
         ref = _request_oracle(kc, vc, bt, r, lens[r], q[r:r + 1], st)
         err = O.compare(ref, out[r:r + 1].cpu())
-        record("c4_sampled", request=r, L=lens[r], **err)
+        record("c4_sampled", request=r, L=lens[r], split=split, **err)
         assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (r, lens[r], err)

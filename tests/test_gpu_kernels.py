@@ -261,17 +261,56 @@ def test_split_counts_agree(S):
     args = (d["q"], dev(kq), dev(vq))
     rest = (d["cu"], d["seq_lens"], d["block_table"], 128 ** -0.5, d["static"])
     T = d["q"].shape[0]
-    os.environ["KVQ_SPLITS"] = "1"
-    try:
-        one = ck.decode_attention(*args, nan_like(d["q"]), *rest, max_query_len=4).cpu()
-    finally:
-        del os.environ["KVQ_SPLITS"]
+    one = ck.decode_attention(*args, nan_like(d["q"]), *rest, max_query_len=4).cpu()
     segm = nan_segm(T, 28, S, 128)
     many = ck.decode_attention(*args, nan_like(d["q"]), *rest, segm=segm, max_query_len=4).cpu()
     err = O.compare(one, many)
     record("split_vs_single", S=S, **err)
     assert err["rel_l2"] < 1e-3 and err["max_abs"] <= 1e-2
     check_attention(oracle_attention(c, kq, vq), many, "split_vs_oracle", S=S)
+
+
+def test_no_split_buffers_means_one_pass_and_no_allocation():
+    """Without split buffers decode_attention / paged_attention (no long requests) cut nothing and take no
+    memory from torch's allocator (the reference runs S = 1 then, kvq/cuda/int8_kv.cu:612-613); the
+    output matches the oracle, long skewed requests included."""
+    c = synth.paged_case(28, 4, [1, 8, 1, 3, 1], [9000, 700, 1, 2100, 33], seed=21, params=synth.channel_params(4, 128))
+    c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    kq_d, vq_d = dev(kq), dev(vq)
+    outs = [nan_like(d["q"]), nan_like(d["q"])]
+    ck.ext()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    ck.decode_attention(d["q"], kq_d, vq_d, outs[0], d["cu"], d["seq_lens"], d["block_table"], c["scale"],
+                        d["static"], max_query_len=8)
+    ck.paged_attention(d["q"], kq_d, vq_d, outs[1], d["cu"], d["seq_lens"], d["block_table"], 8, c["scale"],
+                       d["static"])
+    torch.cuda.synchronize()
+    assert torch.cuda.max_memory_allocated() == before and torch.cuda.memory_allocated() == before
+    ref = oracle_attention(c, kq, vq)
+    for i, o in enumerate(outs):
+        check_attention(ref, o, "one_pass_no_alloc", call=i)
+    assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("reported", [1, 3])
+def test_split_merge_covers_underreported_max_query_len(reported):
+    """A caller that reports a smaller max_query_len than the batch holds still gets every row of every
+    cut request merged (the merge grid walks all query tokens of a request)."""
+    c = synth.paged_case(28, 4, [8, 5, 8, 1], [6000, 4100, 300, 5000], seed=31, params=synth.channel_params(4, 128))
+    c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    T = d["q"].shape[0]
+    out = ck.decode_attention(d["q"], dev(kq), dev(vq), nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
+                              c["scale"], d["static"], segm=nan_segm(T, 28, 32, 128), max_query_len=reported)
+    assert torch.isfinite(out.float()).all()
+    check_attention(oracle_attention(c, kq, vq), out, "underreported_max_query_len", reported=reported)
 
 
 # ------------------------------------------------------------------ mixed batches (long path)
@@ -439,12 +478,8 @@ def test_every_worker_count_covers_the_batch(serving, target_waves, splits):
     os.environ["KVQ_TARGET_WAVES"] = str(target_waves)
     try:
         if splits == 1:
-            os.environ["KVQ_SPLITS"] = "1"
-            try:
-                out = ck.decode_attention(d["q"], kq, vq, nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
-                                          c["scale"], d["static"], max_query_len=73)
-            finally:
-                del os.environ["KVQ_SPLITS"]
+            out = ck.decode_attention(d["q"], kq, vq, nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
+                                      c["scale"], d["static"], max_query_len=73)
         else:
             out = ck.decode_attention(d["q"], kq, vq, nan_like(d["q"]), d["cu"], d["seq_lens"], d["block_table"],
                                       c["scale"], d["static"], segm=nan_segm(T, 12, splits, 128), max_query_len=73)
