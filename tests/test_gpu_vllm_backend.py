@@ -2,7 +2,8 @@
 149-184): the step's K/V are written into vLLM's interleaved int8 cache by do_kv_cache_update (codes
 bit-exact against the oracle), and forward() answers a mixed batch -- decode rows, speculative
 verification rows, long prefill rows -- through the metadata builder's plan and split buffers, within
-the attention bars against the oracle. vLLM itself is replaced by tests/vllm_stub."""
+the attention bars against the oracle -- with vLLM's split buffers (few requests) and without them (more
+requests or tokens than the buffers hold: one pass). vLLM itself is replaced by tests/vllm_stub."""
 import os
 import sys
 from types import SimpleNamespace
@@ -25,12 +26,22 @@ DEV = "cuda"
 HQ, HKV, D, BS = 28, 4, 128, 16
 
 
+BATCHES = {
+    # decode, verification and long prefill rows: more tokens than the split buffers' rows -> one pass
+    "mixed": ([1, 4, 1, 40, 1, 8, 130, 1], [700, 64, 1, 40, 2049, 300, 500, 33], False),
+    # few short requests: vLLM's split buffers are passed (the split path)
+    "short_split": ([1, 4, 1, 8, 1, 3, 1, 1], [700, 64, 1, 2300, 2049, 300, 5000, 33], True),
+    # more requests than seq_threshold_3D (128 // 4 kv heads = 32): no buffers -> one pass
+    "many_decode": ([1] * 38 + [5, 20], [int(x) for x in synth.rng(5).integers(1, 4000, 38)] + [900, 700], False),
+}
+
+
+@pytest.mark.parametrize("batch", list(BATCHES))
 @pytest.mark.parametrize("cfg", ["B_channel_smooth", "B_head"])
-def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg):
+def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg, batch):
     per_channel = cfg.startswith("B_channel")
     smooth = cfg.endswith("smooth")
-    q_lens = [1, 4, 1, 40, 1, 8, 130, 1]
-    seq_lens = [700, 64, 1, 40, 2049, 300, 500, 33]
+    q_lens, seq_lens, with_buffers = BATCHES[batch]
     B = len(q_lens)
     rng = synth.rng(77)
     c = synth.paged_case(HQ, HKV, q_lens, seq_lens, seed=31, params=synth.channel_params(HKV, D))
@@ -45,7 +56,8 @@ def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg):
 
     impl = backend.Int8StaticImpl(HQ, D, D ** -0.5, HKV, kv_cache_dtype="int8_static")
     vcfg = SimpleNamespace(compilation_config=SimpleNamespace(static_forward_context={name: SimpleNamespace(impl=impl)}),
-                           speculative_config=None, model_config=SimpleNamespace(num_heads=HQ, head_size=D),
+                           speculative_config=None,
+                           model_config=SimpleNamespace(num_heads=HQ, num_kv_heads=HKV, head_size=D),
                            scheduler_config=SimpleNamespace(max_num_seqs=64))
     builder = backend.Int8StaticBuilder(SimpleNamespace(block_size=BS), [name], vcfg, DEV)
 
@@ -76,8 +88,10 @@ def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg):
                                      num_actual_tokens=int(cu[-1]), max_query_len=max(q_lens), max_seq_len=max(seq_lens),
                                      block_table_tensor=bt.to(DEV), slot_mapping=slots.to(DEV))
     md = builder.build(0, common)
-    assert md.kvq_long is not None and md.kvq_long.has_short
+    has_long = max(q_lens) > 8
+    assert (md.kvq_long is not None) == has_long and (not has_long or md.kvq_long.has_short)
     T = int(cu[-1])
+    assert (impl._split_buffers(md, T, B) is not None) == with_buffers
     q = c["q"].to(DEV)
     out = nan_like(torch.empty(T + 3, HQ, D, dtype=torch.bfloat16, device=DEV))   # vLLM pads the output
     impl.forward(None, q, None, None, kv_cache, md, out)
@@ -87,7 +101,8 @@ def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg):
     short = torch.repeat_interleave(torch.tensor(q_lens) <= 8, torch.tensor(q_lens))
     got = out[:T].cpu()
     err_s = O.compare(ref[short], got[short])
-    err_l = O.compare(ref[~short], got[~short])
-    record("vllm_backend_step", cfg=cfg, short=err_s, long=err_l)
+    err_l = O.compare(ref[~short], got[~short]) if has_long else None
+    record("vllm_backend_step", cfg=cfg, batch=batch, short=err_s, long=err_l if has_long else None)
     assert err_s["max_abs"] <= 2e-2 and err_s["mean_abs"] <= 2e-3 and err_s["rel_l2"] < 5e-3, err_s
-    assert err_l["rel_l2"] < 1e-2, err_l          # long rows: bf16 attention on dequantized pages
+    if has_long:
+        assert err_l["rel_l2"] < 1e-2, err_l      # long rows: bf16 attention on dequantized pages

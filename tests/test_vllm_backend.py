@@ -29,7 +29,7 @@ def _env(monkeypatch):
     for v in ("KVQ_CFG", "KVQ_KERNEL", "KVQ_SCALES", "KVQ_DRAFT_SCALES", "KVQ_CAPTURE", "KVQ_ATTN", "KVQ_MLA"):
         monkeypatch.delenv(v, raising=False)
     vdist.TP_RANK, vdist.TP_SIZE = 0, 1
-    backend._SCALES_CACHE.clear()
+    backend.SCALE_FILES.clear()
     yield
     vdist.TP_RANK, vdist.TP_SIZE = 0, 1
 
@@ -125,6 +125,22 @@ def test_cache_views_split_the_interleaved_layout(monkeypatch):
     assert kc[2, 5, 1, 7] == kv[2, 1, 5, 7] and vc[2, 5, 1, 7] == kv[2, 1, 5, D + 7]
 
 
+def test_split_buffers_follow_the_triton_builders_rule(monkeypatch):
+    """forward passes vLLM's split buffers only to batches that fit them: at most seq_threshold_3D
+    requests (128 // kv heads) and no more tokens than the buffers' rows; otherwise the INT8 kernel
+    runs in one pass (reference backend.py:175-177)."""
+    from vllm.v1.attention.backends.triton_attn import TritonAttentionMetadataBuilder
+    b = TritonAttentionMetadataBuilder(SimpleNamespace(block_size=BS), [], _vllm_config({}), "cpu")
+    assert b.seq_threshold_3D == 128 // HKV == b.softmax_segm_max.shape[0]
+    md = b.build(0, _common([1] * 4, [10] * 4))
+    impl = _impl(monkeypatch=monkeypatch)
+    bufs = impl._split_buffers(md, 4, 4)
+    assert bufs[0] is b.softmax_segm_output and bufs[1] is b.softmax_segm_max and bufs[2] is b.softmax_segm_expsum
+    assert impl._split_buffers(md, 32, 32) is not None
+    assert impl._split_buffers(md, 33, 33) is None          # more requests than the threshold
+    assert impl._split_buffers(md, 40, 3) is None           # more tokens than the buffers' rows
+
+
 def test_forward_profiling_run_zeroes_output(monkeypatch):
     impl = _impl(monkeypatch=monkeypatch)
     out = torch.ones(4, HQ, D)
@@ -136,7 +152,7 @@ def _vllm_config(layers, spec_tokens=None, max_num_seqs=32):
     ctx = {name: SimpleNamespace(impl=impl) for name, impl in layers.items()}
     spec = None if spec_tokens is None else SimpleNamespace(num_speculative_tokens=spec_tokens)
     return SimpleNamespace(compilation_config=SimpleNamespace(static_forward_context=ctx), speculative_config=spec,
-                           model_config=SimpleNamespace(num_heads=HQ, head_size=D),
+                           model_config=SimpleNamespace(num_heads=HQ, num_kv_heads=HKV, head_size=D),
                            scheduler_config=SimpleNamespace(max_num_seqs=max_num_seqs))
 
 
@@ -241,3 +257,49 @@ def test_capture_statistics_feed_from_stats(monkeypatch):
     smp = capture.collect()["samples"][layer.layer_name]
     assert smp["k"].shape[0] == k.shape[0] and smp["k"].dtype == torch.float16   # under the sample budget
     capture.reset()
+
+
+def test_merge_tp_rebuilds_the_model_wide_heads():
+    """Each rank recorded its own kv heads; merging puts them back in head order (stats rows, sample
+    columns) and keeps one replica when heads are replicated over ranks."""
+    def rank(r, heads):
+        h = torch.tensor(heads, dtype=torch.float32)[:, None].expand(-1, 3)
+        return {"tp_rank": r, "stats": {"l": {"tokens": 5, "k_absmax": h.clone(), "v_absmax": h + 100}},
+                "samples": {"l": {"k": h[None].expand(2, -1, -1).clone(), "v": h[None].expand(2, -1, -1) + 100}}}
+    st, smp = scales.merge_tp([rank(1, [2, 3]), rank(0, [0, 1])], 4)                 # 4 heads over 2 ranks
+    assert st["l"]["k_absmax"][:, 0].tolist() == [0, 1, 2, 3] and st["l"]["tokens"] == 5
+    assert smp["l"]["v"][0, :, 0].tolist() == [100, 101, 102, 103]
+    st, smp = scales.merge_tp([rank(r, [r * 2 // 4]) for r in (3, 2, 1, 0)], 2)     # 2 heads over 4 ranks
+    assert st["l"]["k_absmax"][:, 0].tolist() == [0, 1] and smp["l"]["k"].shape == (2, 2, 3)
+    st, _ = scales.merge_tp([rank(0, [0, 1, 2, 3])], 4)
+    assert st["l"]["k_absmax"].shape == (4, 3)
+
+
+def test_from_stats_quantile_of_the_samples():
+    """q<frac> scales: the round(frac * tokens)-th smallest |x| per channel over the samples (here |x| runs
+    1..200 in every channel, so q0.9 picks 180 and q1.0 the maximum), K centred on its mean first."""
+    vals = torch.arange(1, 201, dtype=torch.float32)
+    sign = torch.where(torch.arange(200) % 2 == 0, 1.0, -1.0)
+    x = (vals * sign)[:, None, None].expand(200, 2, 3).clone()
+    st = {"tokens": torch.tensor(200.0), "k_sum": torch.full((2, 3), 200.0 * 7), "k_max": x.amax(0) + 7,
+          "k_min": x.amin(0) + 7, "k_absmax": (x + 7).abs().amax(0), "v_absmax": x.abs().amax(0)}
+    out = scales.from_stats(st, {"k": x + 7, "v": x}, method="q0.9", smooth_k=True)
+    assert torch.allclose(out["k_mu"], torch.full((2, 3), 7.0))
+    assert torch.equal(out["k_scale"], torch.full((2, 3), 180.0) / 127) and torch.equal(out["v_scale"], out["k_scale"])
+    full = scales.from_stats(st, {"k": x + 7, "v": x}, method="q1.0", granularity="per_head")
+    assert torch.equal(full["v_scale"], torch.full((2, 1), 200.0) / 127) and "k_mu" not in full
+    with pytest.raises(ValueError):
+        scales.from_stats(st, method="p99")
+    with pytest.raises(ValueError):
+        scales.from_stats(st, granularity="per_token")
+
+
+def test_scale_file_keys_and_layer_names_with_separators(tmp_path):
+    """'<layer>|<field>' keys; layer names with dots round-trip, unknown fields are refused."""
+    d = {"draft_model.model.layers.3.self_attn.attn": {"k_scale": torch.ones(2, 1), "v_scale": torch.ones(2, 1)}}
+    p = str(tmp_path / "a.safetensors")
+    scales.save(p, d)
+    back = scales.load(p)
+    assert list(back) == list(d) and torch.equal(back[next(iter(d))]["k_scale"], torch.ones(2, 1))
+    with pytest.raises(ValueError):
+        scales.save(p, {"l": {"k_scales": torch.ones(1, 1)}})

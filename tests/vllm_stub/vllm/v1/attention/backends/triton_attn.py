@@ -8,6 +8,7 @@ import torch
 from vllm.v1.attention.backend import AttentionCGSupport
 
 NUM_SEGMENTS = 16
+MIN_LAUNCH_GRID_SIZE_2D = 128   # the Triton backend uses its split-KV (3D) kernel below this many programs
 
 
 class TritonAttentionBackend:
@@ -65,8 +66,10 @@ class TritonAttentionMetadataBuilder:
         self.device = device
         self.block_size = kv_cache_spec.block_size
         mc = vllm_config.model_config
-        self.seq_threshold_3D = vllm_config.scheduler_config.max_num_seqs
-        rows = vllm_config.scheduler_config.max_num_seqs
+        # as vLLM's Triton builder: batches of up to MIN_LAUNCH_GRID_SIZE_2D // kv heads requests get the
+        # split-KV buffers, which hold that many query rows; larger batches get none
+        self.seq_threshold_3D = MIN_LAUNCH_GRID_SIZE_2D // mc.num_kv_heads
+        rows = self.seq_threshold_3D
         self.softmax_segm_output = torch.empty(rows, mc.num_heads, NUM_SEGMENTS, mc.head_size, dtype=torch.float32,
                                                device=device)
         self.softmax_segm_max = torch.empty(rows, mc.num_heads, NUM_SEGMENTS, dtype=torch.float32, device=device)
