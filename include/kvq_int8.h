@@ -92,6 +92,29 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
                               int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
 
+/* kvq_int8_decode_attention without split buffers from the caller and without any allocation: no
+ * counterpart in the reference. For callers that cannot allocate device memory around the call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * results as kvq_int8_decode_attention with num_splits pieces, except that the split partials live in
+ * a device array of the library (kvq_noalloc_scratch_bytes() bytes, 64 MiB, per GPU, held until the
+ * process ends) instead of segm_out / segm_max / segm_sum; num_tokens (rows of q / out) sizes them.
+ * Rejected (KVQ_ERR_ARG) when num_tokens * num_q_heads * num_splits * (head_dim + 2) * 4 bytes exceed
+ * that array; num_splits == 1 uses none of it. Calls on one GPU share the array: calls that overlap
+ * on one GPU (concurrent streams or threads) race and must be serialised by the caller. */
+int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens,
+                                      const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                                      const int8_t* v_cache, int64_t v_sb, int64_t v_sn, int64_t v_sh,
+                                      int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+                                      void* out, int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q,
+                                      const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                                      int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                                      double softmax_scale, int64_t num_splits, int64_t target_waves,
+                                      int64_t max_query_len, int64_t qmax, void* stream);
+
+/* Size in bytes of the device array kvq_int8_decode_attention_noalloc keeps its split partials in. */
+int kvq_noalloc_scratch_bytes(void);
+
 /* Dequantize pages of the INT8 cache into a contiguous bf16 cache [P, bs, H, D] (long-query path).
  * Replaces the pybind op dequant_pages (reference kvq/cuda/int8_kv.cu:650-672, kernel :505-542),
  * called from kvq/cuda_kernels.py:120-122. Output page p is page src_j[p] of request src_req[p]:

@@ -2017,6 +2017,13 @@ int resident_waves(const void* k, int threads, size_t lds) {
   return w;
 }
 
+// Split partials of kvq_int8_decode_attention_noalloc: [T, Hq, S, D] outputs, then [T, Hq, S] maxima
+// and denominators, in the library's own device array (see `scratch` below). 64 MiB holds, e.g.,
+// 128 tokens x 28 q heads x 35 splits, or 512 x 28 x 9, at head_dim 128.
+constexpr int64_t NOALLOC_SCRATCH_BYTES = 64ll << 20;
+constexpr int MAX_DEVICES = 64;
+char* scratch_ptr();
+
 int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb, int64_t k_sn,
                      int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn, int64_t v_sh, int64_t num_blocks,
                      int64_t block_size, int64_t num_kv_heads, int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
@@ -2025,6 +2032,40 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
                      float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
                      int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
+
+}  // namespace
+
+// The allocation-free decode attention's split partials. Every GPU the library runs on holds one copy
+// for the life of the process; all kvq_int8_decode_attention_noalloc calls on a GPU share it, so calls
+// that overlap on one GPU (two streams, two threads) race. Nothing in it needs clearing between calls:
+// the attention kernel writes every slot the merge kernel reads in the same call.
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device with that device
+// current (each GPU holds its own copy at its own address; in host code the array's name is only a
+// handle for this lookup). nullptr, with the error text set, if the runtime cannot tell.
+char* scratch_ptr() {
+  static std::mutex mu;
+  static char* ptrs[MAX_DEVICES] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    g_err = "int8_decode_attention_noalloc: no current HIP device";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> guard(mu);
+  if (!ptrs[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      g_err = std::string("int8_decode_attention_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    ptrs[dev] = static_cast<char*>(p);
+  }
+  return ptrs[dev];
+}
 
 }  // namespace
 
@@ -2084,7 +2125,7 @@ int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t work
   return launched("stream_read");
 }
 
-int kvq_abi_version(void) { return 4; }
+int kvq_abi_version(void) { return 5; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 
@@ -2193,6 +2234,47 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
                           segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax, stream);
 }
+
+int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens,
+                                      const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t k_sh,
+                                      const int8_t* v_cache, int64_t v_sb, int64_t v_sn, int64_t v_sh,
+                                      int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+                                      void* out, int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q,
+                                      const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                                      int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                                      double softmax_scale, int64_t num_splits, int64_t target_waves,
+                                      int64_t max_query_len, int64_t qmax, void* stream) {
+  if (num_splits < 1 || num_splits > MAX_SPLITS) return fail("int8_decode_attention_noalloc: at most %d split-KV segments", MAX_SPLITS);
+  if (num_tokens < 0 || num_q_heads <= 0 || (head_dim != 64 && head_dim != 128))
+    return fail("int8_decode_attention_noalloc: bad sizes T=%lld Hq=%lld D=%lld", (long long)num_tokens,
+                (long long)num_q_heads, (long long)head_dim);
+  float *so = nullptr, *sm = nullptr, *ss = nullptr;
+  int64_t st_t = 0, st_h = 0;
+  if (num_splits > 1) {
+    // [T, Hq, S, D] partial outputs, then [T, Hq, S] maxima and [T, Hq, S] denominators
+    const int64_t rows = num_tokens * num_q_heads * num_splits;
+    const int64_t need = rows * (head_dim + 2) * (int64_t)sizeof(float);
+    if (num_tokens > INT32_MAX || need > (int64_t)NOALLOC_SCRATCH_BYTES)
+      return fail("int8_decode_attention_noalloc: %lld tokens x %lld q heads x %lld splits need %lld bytes of split "
+                  "partials, more than the library's %lld-byte scratch; pass fewer splits (1 needs none)",
+                  (long long)num_tokens, (long long)num_q_heads, (long long)num_splits, (long long)need,
+                  (long long)NOALLOC_SCRATCH_BYTES);
+    char* base = scratch_ptr();
+    if (!base) return KVQ_ERR_LAUNCH;  // g_err set by scratch_ptr
+    so = reinterpret_cast<float*>(base);
+    sm = so + rows * head_dim;
+    ss = sm + rows;
+    st_t = num_q_heads * num_splits;
+    st_h = num_splits;
+  }
+  return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
+                          num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
+                          num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, so, sm,
+                          ss, st_t, st_h, num_splits, target_waves, max_query_len, qmax, stream);
+}
+
+int kvq_noalloc_scratch_bytes(void) { return (int)NOALLOC_SCRATCH_BYTES; }
 
 }  // extern "C"
 
