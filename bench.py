@@ -150,7 +150,8 @@ def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
     sys.path.insert(0, REPO)
     from oracle import kvq_oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    # every core this process may run on (its affinity mask, which a container's CPU share sets)
+    threads = len(os.sched_getaffinity(0)) or 1
     torch.set_num_threads(threads)
     st = {k: v.cpu() for k, v in w["st"].items()}
     f = O.paged_static_attention(O.CFG32_Q32, st, True, 8)
@@ -171,6 +172,17 @@ def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
         e = O.compare(ref, out[r:r + 1].cpu())
         errs.append(e)
         n += 1
+    # one request on one thread
+    r = 0
+    ids = w["bt"][r, :pages].long()
+    kq, vq, q = w["kc"][ids].cpu(), w["vc"][ids].cpu(), w["q"][r:r + 1].cpu()
+    bt = torch.arange(pages, dtype=torch.int32)[None]
+    sl = torch.tensor([w["L"]], dtype=torch.int32)
+    torch.set_num_threads(1)
+    t0 = time.perf_counter()
+    f(q.float(), kq, vq, one, sl, bt, w["d"] ** -0.5)
+    t1_us = (time.perf_counter() - t0) * 1e6
+    torch.set_num_threads(threads)
     parity = {"requests_checked": n, "max_abs": max(e["max_abs"] for e in errs),
               "mean_abs": statistics.mean(e["mean_abs"] for e in errs),
               "rel_l2_max": max(e["rel_l2"] for e in errs), "bar": "max_abs<=2e-2, mean_abs<=2e-3"}
@@ -179,7 +191,10 @@ def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
     res = {"value": round(kv_bytes / t_total / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
            "sample": f"{n} whole c2 requests (32768 keys, 28/4/128) through the oracle's implementation B "
                      f"(float64) + run_paged on the host, {t_total:.1f} s; KV bytes / s",
-           "us_per_request": round(t_total / n * 1e6, 1), "small_configs": cpu_small_configs(O, threads)}
+           "us_per_request": round(t_total / n * 1e6, 1), "os_cpu_count": os.cpu_count(),
+           "one_thread": {"us_per_request": round(t1_us, 1),
+                          "GBps": round(w["L"] * w["hkv"] * w["d"] * 2 / (t1_us * 1e-6) / 1e9, 4)},
+           "small_configs": cpu_small_configs(O, threads)}
     torch.set_num_threads(threads)
     return res, parity
 
@@ -268,6 +283,28 @@ def _median_event_ms(fn, reps, rotate, calls=20):
     return statistics.median(a.elapsed_time(b) for a, b in evs) / calls
 
 
+def rw_floor(read_bytes, write_bytes, reps=20):
+    """Device time of a plain in-order stream that reads `read_bytes` and writes `write_bytes` (the
+    library's kvq_stream_rw probe), under the same graph-replay protocol as the kernels it bounds, with
+    enough distinct buffer sets to exceed the 256 MB last-level cache; the best of 4, 8 and 16
+    workgroups per CU. Returns (us, workgroups per CU)."""
+    sets = max(1, -(-300 * 2 ** 20 // (read_bytes + write_bytes)))
+    bufs = [(torch.empty(read_bytes // 4, dtype=torch.int32, device=DEV).random_(),
+             torch.empty(write_bytes // 4, dtype=torch.int32, device=DEV)) for _ in range(sets)]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    best = None
+    for per_cu in (4, 8, 16):
+        def fn(i, wg=cus * per_cu):
+            src, dst = bufs[i]
+            _native.call("kvq_stream_rw", src.data_ptr(), read_bytes, dst.data_ptr(), write_bytes, wg,
+                         torch.cuda.current_stream().cuda_stream)
+        ms = _median_event_ms(fn, reps, sets)
+        if best is None or ms < best[0]:
+            best = (ms, per_cu)
+    del bufs
+    return best[0] * 1e3, best[1]
+
+
 def bench_c1(reps=20):
     """Fused quantize + cache write, 16384 tokens x 4 x 128, ~2% padding, 4096 x 16 interleaved cache.
     4 distinct input/cache sets (~400 MB) are rotated to defeat the 256 MB last-level cache."""
@@ -286,8 +323,17 @@ def bench_c1(reps=20):
         ck.quant_reshape_and_cache(k, v, kc, vc, sl, st)
 
     ms = _median_event_ms(fn, reps, len(sets))
+    del sets
+    # the floor: a plain in-order stream of the same bytes (K/V rows read, codes written)
+    f_us, f_wg = rw_floor(t_valid * 2048, t_valid * 1024)
     return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
-            "alg_bytes": alg, "tokens": T, "valid": t_valid}
+            "alg_bytes": alg, "tokens": T, "valid": t_valid,
+            "ceiling": {"us": round(f_us, 2), "GBps": round((t_valid * 3072) / f_us / 1e3, 1),
+                        "frac_of_peak": round((t_valid * 3072) / f_us / 1e3 / PEAK_GBS, 4),
+                        "kernel_vs_ceiling": round(ms * 1e3 / f_us, 3),
+                        "how": "kvq_stream_rw: %d B read + %d B written in order (c1's K/V rows and codes, no slot "
+                               "scatter, no arithmetic), %d workgroups per CU, same graph replay and rotation"
+                               % (t_valid * 2048, t_valid * 1024, f_wg)}}
 
 
 def bench_c3(reps=20, one_pass=True):
@@ -371,12 +417,21 @@ def bench_c4(reps=10, one_pass=True):
     ms_pf = _median_event_ms(lambda i: ck.ext().paged_prefill_attention(qp, kt_p, vt_p, op, cu_pd, sl_pd, bt_p, tr, tw,
                                                                         d ** -0.5), max(3, reps // 2), 1, calls=3)
     pf_flop = sum(L * (L + 1) // 2 for L in pre) * hq * d * 4
+    del kt_p, vt_p
+    dq_read = P * bs * hkv * d * 2
+    f_us, f_wg = rw_floor(dq_read, 2 * dq_read, reps=reps)
     dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
     dq_alg = P * bs * hkv * d * 2 * (1 + 2) + P * 12
     return {"decode_us": round(ms_dec * 1e3, 2), "decode_GBps": round(dec_alg / ms_dec / 1e6, 1),
             "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4), "decode_one_pass_us": round(ms_dec1 * 1e3, 2),
             "dequant_us": round(ms_dq * 1e3, 2), "dequant_GBps": round(dq_alg / ms_dq / 1e6, 1),
             "dequant_frac": round(dq_alg / ms_dq / 1e6 / PEAK_GBS, 4), "dequant_pages": P,
+            "dequant_ceiling": {"us": round(f_us, 2), "GBps": round(3 * dq_read / f_us / 1e3, 1),
+                                "frac_of_peak": round(3 * dq_read / f_us / 1e3 / PEAK_GBS, 4),
+                                "kernel_vs_ceiling": round(ms_dq * 1e3 / f_us, 3),
+                                "how": "kvq_stream_rw: %d B read + %d B written in order (the pages' codes and their "
+                                       "bf16 values, no page gather, no arithmetic), %d workgroups per CU"
+                                       % (dq_read, 2 * dq_read, f_wg)},
             "prefill_ms": round(ms_pf, 3), "prefill_TFLOPs": round(pf_flop / ms_pf / 1e9, 1),
             "prefill_frac_bf16": round(pf_flop / ms_pf / 1e9 / PEAK_BF16_TFLOPS, 4), "prefill_flop": pf_flop}
 

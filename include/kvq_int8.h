@@ -92,6 +92,24 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
                               int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
 
+/* kvq_int8_decode_attention with a choice of q scale granularity: q_group = head_dim is that entry
+ * point's one scale per (token, q head); q_group = 32 quantizes q with one scale per 32 channels and
+ * sums the groups' scaled integer dots in fp32 -- the reference's numerics configurations
+ * B_channel_qgroup32 / B_channel_smooth_qgroup32 (q_gran "group32", kvq/int8_ref.py:120-129), which its
+ * CUDA kernel does not implement (kvq/vllm_int8/backend.py:125-128 rejects them); bound by
+ * kvq/cuda_kernels.py decode_attention / paged_attention(q_group=32). Other arguments and results as
+ * kvq_int8_decode_attention. */
+int kvq_int8_decode_attention_qgroup(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                                     int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                                     int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                     int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                                     double softmax_scale, float* segm_out, float* segm_max, float* segm_sum,
+                                     int64_t seg_st, int64_t seg_sh, int64_t num_splits, int64_t target_waves,
+                                     int64_t max_query_len, int64_t qmax, int64_t q_group, void* stream);
+
 /* kvq_int8_decode_attention without split buffers from the caller and without any allocation: no
  * counterpart in the reference. For callers that cannot allocate device memory around the call (code
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments and
@@ -161,6 +179,16 @@ int kvq_set_attention_events(void* start, void* stop);
  * streaming-read rate HBM sustains on the device, the ceiling bench.py reports beside the attention
  * kernel. Stream-ordered, allocates nothing. */
 int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t workgroups, void* stream);
+
+/* Instrumentation, no counterpart in the reference: reads `read_bytes` at `src` and writes `write_bytes`
+ * at `dst` once, in order, with `workgroups` workgroups of 256 lanes (each a contiguous share of both,
+ * the two streams interleaved in the fixed ratio of their sizes; non-temporal loads and stores; the
+ * written values depend on what was read). The sizes are multiples of 16 bytes in the ratio 2 : 1,
+ * 1 : 1 or 1 : 2 (KVQ_ERR_ARG otherwise). Timing it at a kernel's byte mix -- 2 : 1 for
+ * kvq_quant_cache, 1 : 2 for kvq_dequant_pages -- gives the cost of a plain stream of those bytes on
+ * the device: the floor bench.py reports beside those kernels. Stream-ordered, allocates nothing. */
+int kvq_stream_rw(const void* src, int64_t read_bytes, void* dst, int64_t write_bytes, int64_t workgroups,
+                  void* stream);
 
 /* Text of the last error on this thread ("" if none). */
 const char* kvq_last_error(void);

@@ -42,6 +42,7 @@ namespace {
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int WAVE = 64;
 constexpr int TILE = 32;          // keys per attention tile = P quantization tile
@@ -57,6 +58,7 @@ constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: 
 constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kernel (4 row tiles filling
                                                // one ring): verification batches time best at 12
 constexpr int DEFAULT_PREFETCH = 3;
+constexpr int DEFAULT_V32_RING = 3;     // verify_kernel's ring slots
 constexpr int NUM_XCDS = 8;
 
 // ------------------------------------------------------------------------------------------------
@@ -1287,6 +1289,507 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Verification-shape attention: more than 32 (token, q head) rows per (request, kv head), e.g. 8
+// speculative tokens x 7 q heads = 56 rows. A workgroup of 2 wavefronts takes a piece of one (request,
+// kv head, group of 64 rows); wavefront w owns rows row0 = 32 w .. 32 w + 31 of the group and the two
+// share each 32-key K/V tile through an LDS ring (wavefront w DMAs keys 16 w .. 16 w + 15 of it).
+// Per tile and wavefront, on the 32x32 int8 MFMA (lane l: n = l % 32, h = l / 32):
+//   QK  S^T[key][row] = K . Q^T   v_mfma_i32_32x32x32_i8 x D/32, A = K (lane: key n, channel half h of
+//       each 32-channel step), B = Q^T (lane: row n, same channels)
+//   the accumulator leaves lane (n, h) with row n and keys 8 j + 4 h + i (j, i < 4; register 4 j + i);
+//   those 16 P codes, packed in register order, are exactly the lane's B operand of
+//   PV  O^T[chan][row] = V^T . P^T   v_mfma_i32_32x32x32_i8 x D/32, A = V^T (lane: channel n of the
+//       32-channel tile, the same 16 keys in the same order, read transposed from LDS)
+//   which leaves lane (n, h) with row n and channels 32 c + 8 j + 4 h + i.
+// Against the 16x16 tiles of attn_kernel a wavefront covers twice the rows per tile, so every per-tile
+// cost that is not per (row, key) or (row, channel) -- the row maximum's lane exchange, the tile scale,
+// LDS addressing, the DMA issue, the barrier -- is paid once per 32 rows. The arithmetic per element is
+// attn_kernel's (implementation B, p_tile 32), so results agree with it to the last bit of each row's
+// fp32 sums in the same order.
+// LDS rows are 16-byte chunks XOR-swizzled per key row (K: (row / 2) % chunks, V: bits 1 and 3 of the
+// row, doubled) so that the K reads (16 rows, one chunk) and the transposing V reads (8 rows x 2
+// chunks per 16 lanes) fall on distinct banks.
+// ------------------------------------------------------------------------------------------------
+constexpr int V32_WAVES = 2;      // wavefronts per workgroup (32 rows each)
+constexpr int V32_GROUP_TILES = 4;  // 16-row tiles per row group (the stream-K plan's unit of rows)
+
+template <int CHR>
+__device__ __forceinline__ int swz_k(int row) { return (row >> 1) & (CHR - 1); }
+template <int CHR>
+__device__ __forceinline__ int swz_v(int row) { return ((((row >> 1) & 1) | (((row >> 3) & 1) << 1)) << 1) & (CHR - 1); }
+
+// code bytes of q: rint(x / s) saturated, from r = rcp(s) with the rounding shortcut of quant8 (exact
+// division for a lane whose quotients come near a half-integer); x holds the lane's N channels. Codes
+// are packed as they are made, so only x and the packed words are live at once.
+template <int N>
+__device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (&out)[N / 4]) {
+  const float r = __builtin_amdgcn_rcpf(s);
+  float worst = 0.f;
+#pragma unroll
+  for (int u = 0; u < N / 4; ++u) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float xe = x[4 * u + i];
+      const float t0 = __builtin_fmaf(xe, r, QC_MAGIC);
+      const float res = __builtin_fmaf(xe, r, -(t0 - QC_MAGIC));
+      worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
+      t[i] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
+    }
+    out[u] = pack_magic4(t[0], t[1], t[2], t[3]);
+  }
+  if (worst >= 0.5f - 0x1p-14f) {
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u)
+      out[u] = pack_magic4(code_exact(x[4 * u], s) + QC_MAGIC, code_exact(x[4 * u + 1], s) + QC_MAGIC,
+                           code_exact(x[4 * u + 2], s) + QC_MAGIC, code_exact(x[4 * u + 3], s) + QC_MAGIC);
+  }
+}
+
+// QG: 0 = one q scale per (token, q head) row (implementation B's per-token-head q); 32 = one per 32
+// channels (int8_ref's q_gran "group32"): QK step s then holds exactly group s's channels, its integer
+// dot is scaled by that group's q scale and the groups' scores are summed in fp32.
+template <int D, int PF, int QG>
+__device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
+                                              int c_begin, int c_end, int wave, bool active, int part, int nparts,
+                                              uint8_t* ring, int lane) {
+  constexpr int KST = D / 32;       // 32-channel QK steps = 32-channel PV tiles
+  constexpr int CHR = D / 16;       // 16-byte chunks per K (or V) row
+  constexpr int RPI = WAVE / CHR;   // rows per DMA instruction
+  constexpr int IPH = 16 / RPI;     // DMA instructions per 16-key half of K (or V)
+  constexpr int SLOT = 2 * TILE * D;
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  seq = __builtin_amdgcn_readfirstlane(seq);
+  tok = __builtin_amdgcn_readfirstlane(tok);
+  qlen = __builtin_amdgcn_readfirstlane(qlen);
+  kvh = __builtin_amdgcn_readfirstlane(kvh);
+  row0 = __builtin_amdgcn_readfirstlane(row0);
+  c_begin = __builtin_amdgcn_readfirstlane(c_begin);
+  c_end = __builtin_amdgcn_readfirstlane(c_end);
+  part = __builtin_amdgcn_readfirstlane(part);
+  nparts = __builtin_amdgcn_readfirstlane(nparts);
+  wave = __builtin_amdgcn_readfirstlane(wave);
+  const int n = lane & 31, h = lane >> 5;
+  const int G = a.G;
+  const int L = a.seq_lens[seq];
+  // both wavefronts run every tile (they fill the ring together and meet at one barrier per tile)
+  if (L <= 0) c_end = c_begin;
+  const int nt = c_end - c_begin;
+  const bool work = L > 0 && active;
+  const int* bt = a.block_table + (int64_t)seq * a.bt_stride;
+  const int bs = 1 << a.lbs;
+  const int8_t* kbase = a.kc + (int64_t)kvh * a.k_sh;
+  const int8_t* vbase = a.vc + (int64_t)kvh * a.v_sh;
+
+  // ---- DMA: wavefront `wave` copies keys 16 wave .. 16 wave + 15 of a tile, K rows then V rows; lane L
+  // of an instruction lands at byte 16 L of its RPI rows: row RPI u + L / CHR of the half, physical chunk
+  // L % CHR, which holds logical chunk (L % CHR) ^ swz(row) ----
+  uint32_t koff[IPH], voff[IPH];
+#pragma unroll
+  for (int u = 0; u < IPH; ++u) {
+    const int rb = lane / CHR, pc = lane % CHR, row = 16 * wave + RPI * u + rb;
+    koff[u] = (uint32_t)(rb * (int)a.k_sn + 16 * (pc ^ swz_k<CHR>(row)));
+    voff[u] = (uint32_t)(rb * (int)a.v_sn + 16 * (pc ^ swz_v<CHR>(row)));
+  }
+  const int64_t kstep = (int64_t)RPI * a.k_sn, vstep = (int64_t)RPI * a.v_sn;
+  auto dma = [&](int c, int st) {
+    // the half's first key; a half past the end re-reads the tile's first half (an in-bounds page)
+    int key0 = c * TILE + 16 * wave;
+    key0 = key0 < L ? key0 : c * TILE;
+    const int idx = __builtin_amdgcn_readfirstlane(key0 >> a.lbs);
+    int p = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[idx]);
+    p = (p >= 0 && p < a.num_blocks) ? p : 0;
+    const int o = key0 & (bs - 1);
+    const int8_t* kb = kbase + (int64_t)p * a.k_sb + (int64_t)o * a.k_sn;
+    const int8_t* vb = vbase + (int64_t)p * a.v_sb + (int64_t)o * a.v_sn;
+    uint8_t* dst = ring + st * SLOT + (16 * wave) * D;
+#pragma unroll
+    for (int u = 0; u < IPH; ++u) {
+      __builtin_amdgcn_global_load_lds((const void*)(kb + u * kstep + koff[u]),
+                                       (__attribute__((address_space(3))) void*)(dst + RPI * u * D), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(vb + u * vstep + voff[u]),
+                                       (__attribute__((address_space(3))) void*)(dst + TILE * D + RPI * u * D), 16,
+                                       0, 0);
+    }
+  };
+  constexpr int NIW = 2 * IPH;   // DMA instructions per wavefront and tile
+  if (nt > 0) {
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) dma(c_begin + min(j, nt - 1), j);
+  }
+
+  // ---- LDS read addresses (slot 0; a slot adds st * SLOT): K of QK step s for lane (key n, half h):
+  // logical chunk 2 s + h of row n; V^T of channel tile c, read t: 16-lane group q = lane / 16,
+  // addressing lane P = lane % 16 points at key 8 (2 t + (P / 2) / 4) + 4 (q / 2) + (P / 2) % 4, bytes
+  // 32 c + 16 (q % 2) + 8 (P % 2): ds_read_b64_tr_b8 then hands lane 8 a + b (a, b < 8 ... of the group)
+  // byte b of the chunks of lanes a, a + 2, ..., a + 14, i.e. channel 32 c + 16 (q % 2) + 8 a + b of
+  // keys 8 (2 t + e / 4) + 4 h + e % 4, e = 0..7 -- the P codes' key order ----
+  const uint32_t lbase = (uint32_t)(uintptr_t)ring;
+  uint32_t ka[KST], va[KST][2];
+#pragma unroll
+  for (int s = 0; s < KST; ++s) ka[s] = lbase + n * D + 16 * ((2 * s + h) ^ swz_k<CHR>(n));
+  {
+    const int q = lane >> 4, P = lane & 15, e = P >> 1;
+#pragma unroll
+    for (int c = 0; c < KST; ++c)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int key = 8 * (2 * t + (e >> 2)) + 4 * (q >> 1) + (e & 3);
+        va[c][t] = lbase + TILE * D + key * D + 16 * ((2 * c + (q & 1)) ^ swz_v<CHR>(key)) + 8 * (P & 1);
+      }
+  }
+
+  // ---- q prologue: lane (row n, half h) holds channels 32 s + 16 h + b of row row0 + n; fold s_k,
+  // one scale per row (the two halves exchange their maxima), quantize ----
+  const int R = row0 + n, rtok = R / G, rh = R % G;
+  static_assert(QG == 0 || QG == 32, "q scales per row or per 32 channels");
+  i32x4 qop[KST];
+  float rs;
+  float rsg[QG ? KST : 1];   // per-group score scales (QG): q scale x K scale x softmax scale x log2 e
+  int lim;
+  {
+    float x[16 * KST];
+    float amax = 0.f;
+    if (rtok < qlen && active) {
+      const uint16_t* qp = a.q + (int64_t)(tok + rtok) * a.q_st + (int64_t)(kvh * G + rh) * a.q_sh + 16 * h;
+#pragma unroll
+      for (int s = 0; s < KST; ++s) {
+        const u32x4 w0 = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+        const u32x4 w1 = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8);
+        const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          x[16 * s + 2 * j] = bf16_lo(wd[j]);
+          x[16 * s + 2 * j + 1] = bf16_hi(wd[j]);
+        }
+      }
+      if (a.ks_pc) {
+        const float* kp = a.ks + kvh * D + 16 * h;
+#pragma unroll
+        for (int s = 0; s < KST; ++s)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float4 f = *reinterpret_cast<const float4*>(kp + 32 * s + 4 * u);
+            x[16 * s + 4 * u] *= f.x; x[16 * s + 4 * u + 1] *= f.y;
+            x[16 * s + 4 * u + 2] *= f.z; x[16 * s + 4 * u + 3] *= f.w;
+          }
+      }
+#pragma unroll
+      for (int e = 0; e < 16 * KST; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16 * KST; ++e) x[e] = 0.f;
+    }
+    const float kpost = (a.ks_pc ? 1.f : a.ks[kvh]) * a.sm_log2;
+    if constexpr (QG == 0) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(amax), __float_as_uint(amax), false, false);
+      amax = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      const float s = __builtin_fmaxf(amax / 127.f, 1e-8f);
+      uint32_t codes[4 * KST];
+      q_codes<16 * KST>(x, s, codes);
+#pragma unroll
+      for (int st = 0; st < KST; ++st) qop[st] = i32x4{(int)codes[4 * st], (int)codes[4 * st + 1],
+                                                        (int)codes[4 * st + 2], (int)codes[4 * st + 3]};
+      rs = s * kpost;
+    } else {
+      // group st: this lane's 16 channels and the other half's 16 (lane ^ 32)
+#pragma unroll
+      for (int st = 0; st < KST; ++st) {
+        float ga = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ga = __builtin_fmaxf(ga, __builtin_fabsf(x[16 * st + e]));
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ga), __float_as_uint(ga), false, false);
+        ga = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        const float s = __builtin_fmaxf(ga / 127.f, 1e-8f);
+        float xs[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xs[e] = x[16 * st + e];
+        uint32_t codes[4];
+        q_codes<16>(xs, s, codes);
+        qop[st] = i32x4{(int)codes[0], (int)codes[1], (int)codes[2], (int)codes[3]};
+        rsg[st] = s * kpost;
+      }
+      rs = 0.f;
+    }
+    lim = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
+  }
+
+  float m = -1e30f, l = 0.f, acc[KST][16];
+#pragma unroll
+  for (int c = 0; c < KST; ++c)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[c][v] = 0.f;
+
+  // One 32-key tile from ring offset `so` (an int, or a compile-time constant: then the reads' immediate).
+  // MASKED: some key of the tile is at or past some row's limit.
+  auto tile = [&](auto masked_t, auto so_t, int c) {
+    constexpr bool MASKED = decltype(masked_t)::value;
+    constexpr bool CT = !std::is_same_v<decltype(so_t), int>;
+    uint32_t so;
+    if constexpr (CT) so = 0;
+    else so = (uint32_t)so_t;
+    constexpr int IMM = [] {
+      if constexpr (CT) return decltype(so_t)::value;
+      else return 0;
+    }();
+    const int n0 = c * TILE;
+    // ---- QK ----
+    i32x4 kop[KST];
+    if constexpr (KST == 4) {
+      asm volatile(
+          "ds_read_b128 %0, %4 offset:%c8\n"
+          "ds_read_b128 %1, %5 offset:%c8\n"
+          "ds_read_b128 %2, %6 offset:%c8\n"
+          "ds_read_b128 %3, %7 offset:%c8\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kop[0]), "=&v"(kop[1]), "=&v"(kop[2]), "=&v"(kop[3])
+          : "v"(ka[0] + so), "v"(ka[1] + so), "v"(ka[2] + so), "v"(ka[3] + so), "i"(IMM)
+          : "memory");
+    } else {
+      asm volatile(
+          "ds_read_b128 %0, %2 offset:%c4\n"
+          "ds_read_b128 %1, %3 offset:%c4\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kop[0]), "=&v"(kop[1])
+          : "v"(ka[0] + so), "v"(ka[1] + so), "i"(IMM)
+          : "memory");
+    }
+    i32x16 sc = {};
+    float sf[QG ? 16 : 1];   // QG: the scores (log2 units), the groups' scaled dots summed in fp32
+    if constexpr (QG == 0) {
+#pragma unroll
+      for (int s = 0; s < KST; ++s) sc = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[s], qop[s], sc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < KST; ++s) {
+        const i32x16 zg = __builtin_amdgcn_mfma_i32_32x32x32_i8(kop[s], qop[s], i32x16{}, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sf[v] = s == 0 ? (float)zg[v] * rsg[0] : __builtin_fmaf((float)zg[v], rsg[s], sf[v]);
+      }
+    }
+    // ---- V^T operands (issued now, consumed after the softmax) ----
+    typedef unsigned long long u64;
+    u64 vw[KST][2];
+    if constexpr (KST == 4) {
+      asm volatile(
+          "ds_read_b64_tr_b8 %0, %8 offset:%c16\n"
+          "ds_read_b64_tr_b8 %1, %9 offset:%c16\n"
+          "ds_read_b64_tr_b8 %2, %10 offset:%c16\n"
+          "ds_read_b64_tr_b8 %3, %11 offset:%c16\n"
+          "ds_read_b64_tr_b8 %4, %12 offset:%c16\n"
+          "ds_read_b64_tr_b8 %5, %13 offset:%c16\n"
+          "ds_read_b64_tr_b8 %6, %14 offset:%c16\n"
+          "ds_read_b64_tr_b8 %7, %15 offset:%c16\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(vw[0][0]), "=&v"(vw[0][1]), "=&v"(vw[1][0]), "=&v"(vw[1][1]), "=&v"(vw[2][0]), "=&v"(vw[2][1]),
+            "=&v"(vw[3][0]), "=&v"(vw[3][1])
+          : "v"(va[0][0] + so), "v"(va[0][1] + so), "v"(va[1][0] + so), "v"(va[1][1] + so), "v"(va[2][0] + so),
+            "v"(va[2][1] + so), "v"(va[3][0] + so), "v"(va[3][1] + so), "i"(IMM)
+          : "memory");
+    } else {
+      asm volatile(
+          "ds_read_b64_tr_b8 %0, %4 offset:%c8\n"
+          "ds_read_b64_tr_b8 %1, %5 offset:%c8\n"
+          "ds_read_b64_tr_b8 %2, %6 offset:%c8\n"
+          "ds_read_b64_tr_b8 %3, %7 offset:%c8\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(vw[0][0]), "=&v"(vw[0][1]), "=&v"(vw[1][0]), "=&v"(vw[1][1])
+          : "v"(va[0][0] + so), "v"(va[0][1] + so), "v"(va[1][0] + so), "v"(va[1][1] + so), "i"(IMM)
+          : "memory");
+    }
+    // ---- online softmax; key of register v = n0 + 8 (v / 4) + 4 h + v % 4 ----
+    bool ok[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) ok[v] = MASKED ? n0 + 8 * (v >> 2) + 4 * h + (v & 3) < lim : true;
+    float tmax;
+    if constexpr (QG == 0) {
+      int mx = INT32_MIN;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = ok[v] ? max(mx, sc[v]) : mx;
+      const auto sw = __builtin_amdgcn_permlane32_swap((unsigned)mx, (unsigned)mx, false, false);
+      mx = max((int)sw[0], (int)sw[1]);
+      // an int8 dot product never reaches INT32_MIN: it marks a row with no visible key in the tile
+      tmax = (MASKED && mx == INT32_MIN) ? -INFINITY : (float)mx * rs;
+    } else {
+      float fx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) fx = ok[v] ? __builtin_fmaxf(fx, sf[v]) : fx;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(fx), __float_as_uint(fx), false, false);
+      tmax = __builtin_fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const bool raise = tmax > m + ATTN_SLACK;
+    const bool rescale = raise && m > -1e29f;   // a piece's first tile has nothing to rescale
+    const float mnew = raise ? tmax : m;
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+    m = mnew;
+    const float pm = __builtin_amdgcn_exp2f(tmax - mnew);  // max of this tile's P (exp2 is monotone)
+    const float ps = __builtin_fmaxf(div127(pm), 1e-30f);
+    const float ri = __builtin_amdgcn_rcpf(ps);
+    uint32_t pw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float t[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int v = 4 * j + i;
+        const float p = QG ? __builtin_amdgcn_exp2f(sf[v] - mnew)
+                           : __builtin_amdgcn_exp2f(__builtin_fmaf((float)sc[v], rs, -mnew));
+        const float c2 = __builtin_fminf(__builtin_fmaf(p, ri, QC_MAGIC), QC_MAGIC + 127.f);
+        t[i] = ok[v] ? c2 : QC_MAGIC;
+      }
+      pw[j] = pack_magic4(t[0], t[1], t[2], t[3]);
+    }
+    const i32x4 pop = i32x4{(int)pw[0], (int)pw[1], (int)pw[2], (int)pw[3]};
+    const float psum = (float)__builtin_amdgcn_sad_u8(pw[3], 0u, __builtin_amdgcn_sad_u8(pw[2], 0u,
+                           __builtin_amdgcn_sad_u8(pw[1], 0u, __builtin_amdgcn_sad_u8(pw[0], 0u, 0u))));
+    l = __builtin_fmaf(psum, ps, l * alpha);
+    if (__any(rescale)) {
+#pragma unroll
+      for (int c = 0; c < KST; ++c)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[c][v] *= alpha;
+    }
+    // ---- PV ----
+#pragma unroll
+    for (int c = 0; c < KST; ++c) {
+      const i32x4 vop = i32x4{(int)(uint32_t)vw[c][0], (int)(uint32_t)(vw[c][0] >> 32), (int)(uint32_t)vw[c][1],
+                              (int)(uint32_t)(vw[c][1] >> 32)};
+      i32x16 z = {};
+      z = __builtin_amdgcn_mfma_i32_32x32x32_i8(vop, pop, z, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[c][v] = __builtin_fmaf((float)z[v], ps, acc[c][v]);
+    }
+  };
+
+  // ---- main loop: one barrier per tile. Tile j sits in slot j % PF; after the barrier (this
+  // wavefront's DMA of tile j has landed, everyone's has, and everyone is done with tile j - 1) slot
+  // (j + PF - 1) % PF takes tile j + PF - 1. Tiles j < j_full have no masked key for any row of this
+  // wavefront (a loop of whole rounds of PF of them, with compile-time slots, then the rest); the two
+  // wavefronts may split their tiles differently but each meets exactly one barrier per tile. ----
+  if (nt > 0) {
+    const int lim_lo = L - qlen + 1 + row0 / G;          // every row of this wavefront sees keys < lim_lo
+    const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
+    const int j_full = work ? max(0, min(nt, full_end - c_begin)) : nt;
+    auto step = [&](auto masked_t, int j, auto st_t) {
+      wait_vm<(PF - 2) * NIW>();
+      lds_barrier();
+      dma(c_begin + min(j + PF - 1, nt - 1), (j + PF - 1) % PF);
+      if (work) {
+        if constexpr (std::is_same_v<decltype(st_t), int>) tile(masked_t, (int)(st_t * SLOT), c_begin + j);
+        else tile(masked_t, std::integral_constant<int, decltype(st_t)::value * SLOT>{}, c_begin + j);
+      }
+    };
+    int j = 0;
+    for (; j + PF <= j_full; j += PF) {
+      step(std::false_type{}, j, std::integral_constant<int, 0>{});
+      if constexpr (PF > 1) step(std::false_type{}, j + 1, std::integral_constant<int, 1 % PF>{});
+      if constexpr (PF > 2) step(std::false_type{}, j + 2, std::integral_constant<int, 2 % PF>{});
+      if constexpr (PF > 3) step(std::false_type{}, j + 3, std::integral_constant<int, 3 % PF>{});
+      static_assert(PF >= 2 && PF <= 4, "rounds are written for 2 to 4 slots");
+    }
+    for (; j < j_full; ++j) step(std::false_type{}, j, j % PF);
+    for (; j < nt; ++j) step(std::true_type{}, j, j % PF);
+    wait_vm<0>();   // the ring is empty and read before the next piece refills it
+    lds_barrier();
+  }
+
+  // ---- epilogue: lane (n, h) holds row n, channels 32 c + 8 j + 4 h + i in acc[c][4 j + i] ----
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
+    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  if (!active || rtok >= qlen) return;
+  const int head = kvh * G + rh;
+  const int qt = tok + rtok;
+  // the V scales of channels 32 c + 8 j + 4 h .. + 3, fetched next to their use
+  auto vscale4 = [&](int c, int j) -> float4 {
+    if (a.vs_pc) return *reinterpret_cast<const float4*>(a.vs + kvh * D + 32 * c + 8 * j + 4 * h);
+    const float v = a.vs[kvh];
+    return float4{v, v, v, v};
+  };
+  if (nparts == 1) {
+    if (a.max_splits > 1 && h == 0) a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
+    const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
+    uint16_t* orow = a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + 4 * h;
+#pragma unroll
+    for (int c = 0; c < KST; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 f = vscale4(c, j);
+        const float* ac = &acc[c][4 * j];
+        *reinterpret_cast<u32x2*>(orow + 32 * c + 8 * j) =
+            u32x2{pack_bf16x2((ac[0] * inv) * f.x, (ac[1] * inv) * f.y), pack_bf16x2((ac[2] * inv) * f.z, (ac[3] * inv) * f.w)};
+      }
+  } else {
+    const int64_t sidx = (int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh + part;
+    if (h == 0) {
+      a.segm_max[sidx] = m;
+      a.segm_sum[sidx] = part == nparts - 1 ? -2.f - l : l;  // the last piece is marked (l >= 0)
+    }
+    float* sp = a.segm_out + sidx * D + 4 * h;
+#pragma unroll
+    for (int c = 0; c < KST; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 f = vscale4(c, j);
+        const float* ac = &acc[c][4 * j];
+        *reinterpret_cast<float4*>(sp + 32 * c + 8 * j) = float4{ac[0] * f.x, ac[1] * f.y, ac[2] * f.z, ac[3] * f.w};
+      }
+  }
+}
+
+// Stream-K over the batch as attn_kernel (plan_and_locate, the same units and pieces), for row groups
+// of 64 rows run by the 2 wavefronts of attend_rows32.
+template <int D, int PF, int QG>
+__global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
+  const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  extern __shared__ float v32_lds[];   // the ring: PF slots of 32 keys' K rows then V rows
+  int worker = blockIdx.x;
+  if (a.xcd_order) {
+    const int q = a.workers / NUM_XCDS, rem = a.workers % NUM_XCDS;
+    const int wx = blockIdx.x % NUM_XCDS, wi = blockIdx.x / NUM_XCDS;
+    worker = wx * q + min(wx, rem) + wi;
+  }
+  if (worker >= a.workers) return;
+  int r;
+  long long rstart;
+  const Plan pl = plan_and_locate(a, worker, lane, r, rstart);
+  long long pos = (long long)worker * pl.chunk;
+  const long long end = min(pos + pl.chunk, pl.total);
+  if (pos >= end || r >= a.num_seqs) return;
+  ReqWork w = req_work(a, r);
+  int seglen = seg_units(a, w);
+  int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
+  const bool whole = a.max_splits == 1;
+  uint8_t* ring = reinterpret_cast<uint8_t*>(v32_lds);
+  while (pos < end) {
+    const long long seg_start = rstart + (long long)seg * seglen;
+    const int take = (int)min((long long)(seglen - off), end - pos);
+    const int fc = a.seg_cost;
+    const long long first = whole ? worker : (seg_start + fc) / pl.chunk;
+    const long long last = whole ? worker : (seg_start + seglen - 1) / pl.chunk;
+    const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
+    const int row0 = rg * (16 * V32_GROUP_TILES) + 32 * wave;
+    const int c0 = whole ? 0 : max(off - fc, 0);
+    const int c1 = whole ? (off == 0 ? w.ntiles : 0) : max(off + take - fc, 0);
+    if (c1 > c0)
+      attend_rows32<D, PF, QG>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, wave, row0 < w.qlen * a.G, (int)(worker - first),
+                           (int)(last - first + 1), ring, lane);
+    pos += take;
+    off = 0;
+    if (++seg == a.hkv * w.rgroups && pos < end) {  // on to the next request with work
+      rstart += (long long)seglen * a.hkv * w.rgroups;
+      seg = 0;
+      do {
+        if (++r >= a.num_seqs) return;
+        w = req_work(a, r);
+      } while (w.ntiles == 0);
+      seglen = seg_units(a, w);
+    }
+  }
+}
+
 // Merge the pieces of the cut segments (reference kvq/cuda/int8_kv.cu:465-503):
 //   o = sum_s 2^(m_s - M) acc_s / max(sum_s 2^(m_s - M) l_s, 1e-30)
 // One wavefront per (request, q head, query token), RED_WAVES q heads per workgroup (fewer, larger
@@ -1912,6 +2415,39 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
   out[(int64_t)blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
+// Streaming read + write probe, no counterpart in the reference: `src` (nr 16-byte chunks) is read
+// once and `dst` (nw chunks) written once, in order, each workgroup a contiguous share of both, the
+// two streams interleaved in the fixed ratio KR : KW (per round a lane reads KR chunks and writes KW,
+// each value a function of what it read). Timed at a kernel's byte mix -- 2 : 1 for the fused cache
+// write (bf16 K/V read, int8 codes written), 1 : 2 for page dequantization (int8 read, bf16 written) --
+// it gives what a plain stream of that many bytes costs on the box, the floor that kernel is compared
+// with.
+template <int KR, int KW>
+__global__ __launch_bounds__(256) void stream_rw_kernel(const u32x4* __restrict__ src, int64_t nr,
+                                                        u32x4* __restrict__ dst, int64_t nw) {
+  constexpr int64_t STEP = 256;   // the workgroup's 256 lanes, one chunk each
+  const int64_t r0 = nr * blockIdx.x / gridDim.x, r1 = nr * (blockIdx.x + 1) / gridDim.x;
+  const int64_t w0 = nw * blockIdx.x / gridDim.x, w1 = nw * (blockIdx.x + 1) / gridDim.x;
+  const int64_t rounds = max((r1 - r0 + KR * STEP - 1) / (KR * STEP), (w1 - w0 + KW * STEP - 1) / (KW * STEP));
+  uint32_t acc = threadIdx.x;
+  for (int64_t rd = 0; rd < rounds; ++rd) {
+    u32x4 v[KR];
+#pragma unroll
+    for (int k = 0; k < KR; ++k) {
+      const int64_t i = r0 + (rd * KR + k) * STEP + threadIdx.x;
+      v[k] = i < r1 ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < KR; ++k) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+#pragma unroll
+    for (int k = 0; k < KW; ++k) {
+      const int64_t i = w0 + (rd * KW + k) * STEP + threadIdx.x;
+      const u32x4 w = v[k % KR];
+      if (i < w1) __builtin_nontemporal_store(u32x4{w.x ^ acc, w.y, w.z ^ (uint32_t)k, w.w}, dst + i);
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Host side: argument checks, launches, error reporting.
 // ------------------------------------------------------------------------------------------------
@@ -1965,6 +2501,14 @@ int lds_prefetch_depth() {
     return v <= 3 ? 3 : (v >= 6 ? 6 : 4);
   }();
   return depth;
+}
+
+// slots of verify_kernel's LDS ring (KVQ_V32_RING: 3 or 4; 3, 4 and 5 time the same on verification
+// batches, 6 is slower)
+int v32_ring_depth() {
+  const char* e = getenv("KVQ_V32_RING");
+  const int v = e ? atoi(e) : DEFAULT_V32_RING;
+  return v <= 3 ? 3 : 4;
 }
 
 // Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
@@ -2031,7 +2575,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
                      int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
                      float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
-                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
+                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, int64_t q_group,
+                     void* stream);
 
 }  // namespace
 
@@ -2125,7 +2670,25 @@ int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t work
   return launched("stream_read");
 }
 
-int kvq_abi_version(void) { return 5; }
+int kvq_stream_rw(const void* src, int64_t read_bytes, void* dst, int64_t write_bytes, int64_t workgroups,
+                  void* stream) {
+  if (!src || !dst || read_bytes < 16 || write_bytes < 16 || read_bytes % 16 || write_bytes % 16 || !aligned16(src) ||
+      !aligned16(dst) || workgroups < 1 || workgroups > INT32_MAX / 256)
+    return fail("stream_rw: need 16-byte aligned buffers of positive multiples of 16 bytes and 1..2^23 workgroups");
+  const int64_t nr = read_bytes / 16, nw = write_bytes / 16;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)workgroups), block(256);
+  const u32x4* s = reinterpret_cast<const u32x4*>(src);
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  if (nr == 2 * nw) hipLaunchKernelGGL((stream_rw_kernel<4, 2>), grid, block, 0, st, s, nr, d, nw);
+  else if (2 * nr == nw) hipLaunchKernelGGL((stream_rw_kernel<2, 4>), grid, block, 0, st, s, nr, d, nw);
+  else if (nr == nw) hipLaunchKernelGGL((stream_rw_kernel<4, 4>), grid, block, 0, st, s, nr, d, nw);
+  else return fail("stream_rw: read : write must be 2 : 1, 1 : 1 or 1 : 2 (got %lld : %lld bytes)", (long long)read_bytes,
+                   (long long)write_bytes);
+  return launched("stream_rw");
+}
+
+int kvq_abi_version(void) { return 7; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 
@@ -2232,7 +2795,27 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
                           num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
-                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax, stream);
+                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax, 0, stream);
+}
+
+int kvq_int8_decode_attention_qgroup(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                                     int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                                     int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                     int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
+                                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                                     double softmax_scale, float* segm_out, float* segm_max, float* segm_sum,
+                                     int64_t seg_st, int64_t seg_sh, int64_t num_splits, int64_t target_waves,
+                                     int64_t max_query_len, int64_t qmax, int64_t q_group, void* stream) {
+  if (q_group != 32 && q_group != head_dim)
+    return fail("int8_decode_attention_qgroup: q_group must be 32 or head_dim (%lld), got %lld", (long long)head_dim,
+                (long long)q_group);
+  return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
+                          num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
+                          num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
+                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax,
+                          q_group == 32 ? 32 : 0, stream);
 }
 
 int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens,
@@ -2271,7 +2854,7 @@ int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh,
   return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
                           num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, so, sm,
-                          ss, st_t, st_h, num_splits, target_waves, max_query_len, qmax, stream);
+                          ss, st_t, st_h, num_splits, target_waves, max_query_len, qmax, 0, stream);
 }
 
 int kvq_noalloc_scratch_bytes(void) { return (int)NOALLOC_SCRATCH_BYTES; }
@@ -2287,7 +2870,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
                      int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
                      float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
-                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream) {
+                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, int64_t q_group,
+                     void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("int8_decode_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("int8_decode_attention: block_size must be a power of two >= 16");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -2315,7 +2899,11 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   const int ks_max = ks_env ? std::max(1, std::min(MAX_ROW_TILES, atoi(ks_env)))
                             : (num_splits == 1 ? MAX_ROW_TILES : DEFAULT_KSPLIT);
   const int ks = std::max(1, std::min(ks_max, MAX_ROW_TILES / rt));
-  const int waves = rt * ks;
+  // more than 32 rows per (request, kv head): the 32-row wavefronts of verify_kernel (KVQ_ROWS32=0: off)
+  // (per-32-channel q scales run there for every row count)
+  const bool rows32 = q_group == 32 ||
+                      ((int64_t)G * maxq > 32 && !(getenv("KVQ_ROWS32") && atoi(getenv("KVQ_ROWS32")) == 0));
+  const int waves = rows32 ? V32_WAVES : rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535 || (num_q_heads + RED_WAVES - 1) / RED_WAVES > 65535 ||
       maxq > 65535)
     return fail("int8_decode_attention: grid too large");
@@ -2332,18 +2920,26 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX);
   a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
-  a.max_splits = (int)num_splits; a.rt = rt; a.ksplit = ks; a.waves = waves;
-  a.min_tiles = MIN_SPLIT_TILES * ks;
+  a.max_splits = (int)num_splits; a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? 1 : ks; a.waves = waves;
+  a.min_tiles = MIN_SPLIT_TILES * a.ksplit;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
-  a.lds_ring = (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0)) ? 1 : 0;
+  a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;
   a.seg_cost = seg_cost_units(a.lds_ring != 0);
-  const int pf = a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
+  const int pf = rows32 ? v32_ring_depth() : a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
   const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
                                 : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
   void (*kern)(AttnArgs);
-  if (a.lds_ring) {
+  if (rows32) {
+    if (q_group == 32) {
+      if (head_dim == 128) kern = pf == 3 ? verify_kernel<128, 3, 32> : verify_kernel<128, 4, 32>;
+      else kern = pf == 3 ? verify_kernel<64, 3, 32> : verify_kernel<64, 4, 32>;
+    } else {
+      if (head_dim == 128) kern = pf == 3 ? verify_kernel<128, 3, 0> : verify_kernel<128, 4, 0>;
+      else kern = pf == 3 ? verify_kernel<64, 3, 0> : verify_kernel<64, 4, 0>;
+    }
+  } else if (a.lds_ring) {
     if (head_dim == 128) kern = pf == 3 ? attn_kernel<128, 3, true> : pf == 6 ? attn_kernel<128, 6, true> : attn_kernel<128, 4, true>;
     else kern = pf == 3 ? attn_kernel<64, 3, true> : pf == 6 ? attn_kernel<64, 6, true> : attn_kernel<64, 4, true>;
   } else if (head_dim == 128) {

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 5
+ABI_VERSION = 7
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -22,6 +22,10 @@ SIGNATURES = {
     "kvq_int8_decode_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _i64,
                                   _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr],
+    "kvq_int8_decode_attention_qgroup": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
+                                         _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr,
+                                         _i64, _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64,
+                                         _i64, _ptr],
     "kvq_int8_decode_attention_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64,
                                           _i64, _ptr, _i64, _ptr, _i64, _f64, _i64, _i64, _i64, _i64, _ptr],
@@ -34,6 +38,7 @@ SIGNATURES = {
     "kvq_prefill_rows_per_tile": [],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_stream_read": [_ptr, _i64, _ptr, _i64, _ptr],
+    "kvq_stream_rw": [_ptr, _i64, _ptr, _i64, _i64, _ptr],
     "kvq_last_error": [],
     "kvq_abi_version": [],
 }

@@ -111,7 +111,7 @@ class _Ext:
 
     # kvq/cuda/int8_kv.cu:600-648
     def int8_decode_attention(self, q, kc, vc, out, cu_q, seq_lens, block_table, ks, vs, softmax_scale, segm_out,
-                              segm_max, segm_sum, max_query_len, qmax):
+                              segm_max, segm_sum, max_query_len, qmax, q_group=None):
         num_seqs, Hq, Hkv = cu_q.shape[0] - 1, q.shape[1], kc.shape[2]
         _check(q.shape[2] == kc.shape[3] and kc.stride(3) == 1 and q.stride(2) == 1, "unsupported shape/layout")
         bs = kc.shape[1]
@@ -150,14 +150,19 @@ class _Ext:
             _check(segm_out.shape[3] == d and segm_out.stride(3) == 1 and segm_out.stride(2) == d and
                    segm_out.stride(1) == seg_sh * d and segm_out.stride(0) == seg_st * d,
                    "int8_decode_attention: segm_out must be laid out as segm_max x head_dim")
-        _native.call("kvq_int8_decode_attention", q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0),
-                     kc.stride(1), kc.stride(2), vc.data_ptr(), vc.stride(0), vc.stride(1), vc.stride(2),
-                     kc.shape[0], bs, Hkv, d, out.data_ptr(), out.stride(0), out.stride(1), cu_q.data_ptr(),
-                     seq_lens.data_ptr(), block_table.data_ptr(), block_table.stride(0), num_seqs, Hq,
-                     ks.data_ptr(), kcols, vs.data_ptr(), vcols, float(softmax_scale),
-                     segm_out.data_ptr() if split else None, segm_max.data_ptr() if split else None,
-                     segm_sum.data_ptr() if split else None, seg_st, seg_sh, S, _target_waves(),
-                     int(max_query_len), int(qmax), _stream(q))
+        _check(q_group in (None, d, 32), f"int8_decode_attention: q scales per row or per 32 channels, not {q_group}")
+        grouped = q_group == 32
+        args = [q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+                vc.data_ptr(), vc.stride(0), vc.stride(1), vc.stride(2), kc.shape[0], bs, Hkv, d, out.data_ptr(),
+                out.stride(0), out.stride(1), cu_q.data_ptr(), seq_lens.data_ptr(), block_table.data_ptr(),
+                block_table.stride(0), num_seqs, Hq, ks.data_ptr(), kcols, vs.data_ptr(), vcols, float(softmax_scale),
+                segm_out.data_ptr() if split else None, segm_max.data_ptr() if split else None,
+                segm_sum.data_ptr() if split else None, seg_st, seg_sh, S, _target_waves(), int(max_query_len),
+                int(qmax)]
+        if grouped:
+            _native.call("kvq_int8_decode_attention_qgroup", *args, 32, _stream(q))
+        else:
+            _native.call("kvq_int8_decode_attention", *args, _stream(q))
 
     # kvq/cuda/int8_kv.cu:650-672
     def dequant_pages(self, kc, vc, ko, vo, block_table, src_req, src_j, ks, vs):
@@ -260,17 +265,21 @@ def _target_waves():
 
 
 def decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, softmax_scale, static,
-                     segm=None, max_query_len=1):
+                     segm=None, max_query_len=1, q_group=None):
     """INT8 attention for the requests with at most SHORT_Q query tokens (others are skipped).
     max_query_len bounds the short queries' length (reference kvq/cuda_kernels.py:51-58).
 
     segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) allows up to S pieces per
     (request, kv head) (the reference always uses S); the kernel gives each as many of them as its share
     of the batch's work calls for. Without segm nothing is cut and nothing is allocated: one pass, each
-    (request, kv head) whole in one workgroup (the reference's S = 1, kvq/cuda/int8_kv.cu:612-613)."""
+    (request, kv head) whole in one workgroup (the reference's S = 1, kvq/cuda/int8_kv.cu:612-613).
+
+    q_group: None (one q scale per (token, q head), the reference kernel's numerics) or 32 (one per 32
+    channels: the B_*_qgroup32 configurations of kvq/int8_ref.py:120-129, an addition to the reference's
+    operator API)."""
     so, sm, ss = segm if segm is not None else (None, None, None)
     ext().int8_decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, static["k_scale"],
-                                static["v_scale"], softmax_scale, so, sm, ss, max_query_len, SHORT_Q)
+                                static["v_scale"], softmax_scale, so, sm, ss, max_query_len, SHORT_Q, q_group)
     return out
 
 
@@ -407,9 +416,9 @@ def check_inputs(q, k_cache, cu_seqlens_q, seq_lens, block_table, plan):
 
 
 def paged_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, max_query_len, softmax_scale,
-                    static, plan=None, segm=None):
+                    static, plan=None, segm=None, q_group=None):
     """Both paths for one batch, as the backend runs them (plan from plan_long, None if all short)
-    (reference kvq/cuda_kernels.py:172-183)."""
+    (reference kvq/cuda_kernels.py:172-183). q_group as decode_attention's (the INT8 rows only)."""
     if os.environ.get("KVQ_DEBUG") == "1":
         check_inputs(q, k_cache, cu_seqlens_q, seq_lens, block_table, plan)
     if plan is not None:
@@ -417,5 +426,5 @@ def paged_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_tabl
                        softmax_scale, static)
     if plan is None or plan.has_short:
         decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, softmax_scale, static,
-                         segm, max_query_len)
+                         segm, max_query_len, q_group)
     return out

@@ -8,7 +8,8 @@ kvq.vllm_plugin registers the class), and
   KVQ_SCALES        calibrated static scales (safetensors, kvq.scales format)
   KVQ_DRAFT_SCALES  scales of a speculative-decoding draft model (layers prefixed "draft_model.")
   KVQ_CFG           numerics name; the kernels implement B_channel_smooth (default), B_channel,
-                    B_head_smooth and B_head (implementation B, per-(token, head) q, per-tile P)
+                    B_head_smooth, B_head (implementation B, per-(token, head) q, per-tile P) and
+                    B_channel_smooth_qgroup32, B_channel_qgroup32 (q scales per 32 channels)
   KVQ_KERNEL        "cuda" (default; the name is kept for compatibility -- it selects these HIP kernels)
 
 Per step and layer the backend
@@ -39,13 +40,16 @@ logger = init_logger("vllm.kvq")  # a child of vLLM's logger, so vLLM's handler 
 
 DEFAULT_CFG = "B_channel_smooth"
 # KVQ_CFG names of the reference's numerics table (kvq/int8_ref.py:201-223) these kernels compute, with
-# the scale layout each implies: (K/V granularity, smooth-K). The table's other names are ablations or
-# implementation-A configurations.
+# what each implies: (K/V scale granularity, smooth-K, q scale group: None = per (token, q head)). The
+# table's other names are ablations or implementation-A configurations.
 KERNEL_CONFIGS = {
-    "B_channel_smooth": ("per_channel", True),
-    "B_channel": ("per_channel", False),
-    "B_head_smooth": ("per_head", True),
-    "B_head": ("per_head", False),
+    "B_channel_smooth": ("per_channel", True, None),
+    "B_channel": ("per_channel", False, None),
+    "B_head_smooth": ("per_head", True, None),
+    "B_head": ("per_head", False, None),
+    # q scales per 32 channels (q_gran "group32", kvq/int8_ref.py:120-129)
+    "B_channel_smooth_qgroup32": ("per_channel", True, 32),
+    "B_channel_qgroup32": ("per_channel", False, 32),
 }
 DRAFT_PREFIX_END = "model.layers"   # a draft layer "draft_model.model.layers.<i>..." is "model.layers.<i>..."
                                     # in the draft's own calibration file
@@ -166,9 +170,9 @@ class Int8StaticImpl(TritonAttentionImpl):
         _check_kernel_choice()
         self.cfg_name = os.environ.get("KVQ_CFG", DEFAULT_CFG)
         assert self.cfg_name in KERNEL_CONFIGS, (
-            f"the INT8 kernels implement B with per-(token, head) q and per-tile P "
+            f"the INT8 kernels implement B with per-(token, head) or per-32-channel q and per-tile P "
             f"({', '.join(KERNEL_CONFIGS)}), not {self.cfg_name}")
-        self.granularity, self.smooth_k = KERNEL_CONFIGS[self.cfg_name]
+        self.granularity, self.smooth_k, self.q_group = KERNEL_CONFIGS[self.cfg_name]
         self.static = None
         cuda_kernels.ext()  # load the library now, at model build time, long before graph capture
 
@@ -218,5 +222,5 @@ class Int8StaticImpl(TritonAttentionImpl):
         segm = self._split_buffers(md, n, md.query_start_loc.shape[0] - 1)
         cuda_kernels.paged_attention(query[:n], k_cache, v_cache, output[:n], md.query_start_loc, md.seq_lens,
                                      md.block_table, md.max_query_len, self.scale, self.static,
-                                     getattr(md, "kvq_long", None), segm)
+                                     getattr(md, "kvq_long", None), segm, q_group=self.q_group)
         return output

@@ -166,6 +166,8 @@ CFG32 = Cfg(smooth_k=True, p_tile=32)
 CFG32_HEAD = Cfg(smooth_k=True, p_tile=32, k_gran="per_head", v_gran="per_head")
 CFG32_Q32 = Cfg(smooth_k=True, p_tile=32, q_arith="fp32")
 CFG32_HEAD_Q32 = Cfg(smooth_k=True, p_tile=32, k_gran="per_head", v_gran="per_head", q_arith="fp32")
+CFG32_G32 = Cfg(smooth_k=True, p_tile=32, q_gran="group32")
+CFG32_G32_Q32 = Cfg(smooth_k=True, p_tile=32, q_gran="group32", q_arith="fp32")
 
 
 def attend_dequant(qb, kq, ks, vq, vs, mask, softmax_scale):
@@ -224,6 +226,8 @@ def attend_int8(qb, kq, ks, vq, vs, mask, softmax_scale, cfg):
     kd = kq.double()
     if cfg.q_gran.startswith("group"):
         n = int(cfg.q_gran[5:])
+        if cfg.q_arith == "fp32":   # the kernel's contract: q' = fl32(q * s_k), fp32 scale and division
+            qf = (qg.float() * ks.float()[:, :, :, None, :]) if ks.shape[-1] > 1 else qg.float()
         qs = qf.reshape(*qf.shape[:-1], qf.shape[-1] // n, n)     # [b, R, Hkv, G, C, n]
         sq = scale_from_absmax(qs.abs().amax(-1, keepdim=True))
         qi = quantize(qs, sq).double()

@@ -49,6 +49,8 @@ def build(name):
 
 NAMES = ["c0_pc", "c0_ph", "short_28_4", "short_14_2_d64", "short_32_8_ph", "edge", "mixed"]
 WITH_BF16_REF = ["c0_pc", "c0_ph", "short_28_4", "mixed"]
+# cases also stored with q scales per 32 channels (int8_ref Cfg(q_gran="group32"), per-channel K)
+WITH_QGROUP32 = ["c0_pc", "short_28_4", "short_14_2_d64", "mixed"]
 
 
 def stored_rows(name, cu):

@@ -6,6 +6,7 @@ It imports the reference's kvq.quant, kvq.ref_attn and kvq.int8_ref (pure PyTorc
 for each case of tests/golden/cases.py:
   <case>|int8_b    (rows of cases.stored_rows) paged_static_attention(Cfg(smooth_k=True, p_tile=32[, per-head]), cache_is_int8=True,
                    short_q=8) output (bf16)  -- kvq/int8_ref.py:162-197, as tests/test_cuda_kernels.py:12-17
+  <case>|int8_b_qgroup32  (cases.WITH_QGROUP32) the same with Cfg(..., q_gran="group32")  -- kvq/int8_ref.py:120-129
   <case>|bf16_ref  paged_attention_ref on the original bf16 K/V (bf16)     -- kvq/ref_attn.py:88-90
   codes sha256     of the int8 caches quant.quantize(k - mu, s_k), quant.quantize(v, s_v)  -- kvq/quant.py:50-51
   quant|codes      quant.quantize on the corner-case inputs of cases.quant_special()
@@ -53,6 +54,11 @@ def main():
         g = ref_attn.paged_attention_ref(c["q"], c["k"], c["v"], *args, c["scale"]) if name in cases.WITH_BF16_REF else None
         rows = cases.stored_rows(name, c["cu"])
         tensors[f"{name}|int8_b"] = b[rows].contiguous()
+        if name in cases.WITH_QGROUP32:
+            cfg_g = ref_int8.Cfg(smooth_k=True, p_tile=32, q_gran="group32")
+            bg = ref_int8.paged_static_attention(cfg_g, st, cache_is_int8=True, short_q=8)(c["q"], kq, vq, *args,
+                                                                                          c["scale"])
+            tensors[f"{name}|int8_b_qgroup32"] = bg[rows].contiguous()
         if name in cases.WITH_BF16_REF:
             tensors[f"{name}|bf16_ref"] = g[rows].contiguous()
         meta["cases"][name] = {"k_codes_sha256": sha(kq), "v_codes_sha256": sha(vq),

@@ -205,6 +205,42 @@ def test_attention_matches_reference_golden(golden, name):
         assert abs(drift["rel_l2"] - ref_drift["rel_l2"]) < 0.01, (drift, ref_drift)
 
 
+@pytest.mark.parametrize("name", cases.WITH_QGROUP32)
+@pytest.mark.parametrize("split", [False, True])
+def test_attention_qgroup32_matches_reference_golden(golden, name, split):
+    """q scales per 32 channels (q_group=32: the B_*_qgroup32 configurations, kvq/int8_ref.py:120-129)
+    against the reference's own output (fixture, rel_l2 bar of the reference's tests) and the oracle's
+    fp32-q group path (strict bar); head_dim 64 and 128, decode to 8-token rows, with and without split
+    buffers, and a mixed batch whose long rows take the dequantize + prefill path."""
+    g, _ = golden
+    c = cases.build(name)
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    out = nan_like(d["q"])
+    T, hq, D = d["q"].shape
+    maxq = int((c["cu"][1:] - c["cu"][:-1]).max())
+    segm = nan_segm(T, hq, 16, D) if split else None
+    if name == "mixed":
+        plan = ck.plan_long(c["cu"], c["seq_lens"], 16)
+        ck.paged_attention(d["q"], dev(kq), dev(vq), out, d["cu"], d["seq_lens"], d["block_table"], maxq, c["scale"],
+                           d["static"], plan, segm, q_group=32)
+    else:
+        ck.decode_attention(d["q"], dev(kq), dev(vq), out, d["cu"], d["seq_lens"], d["block_table"], c["scale"],
+                            d["static"], segm=segm, max_query_len=maxq, q_group=32)
+    rows = cases.stored_rows(name, c["cu"])
+    o = out.cpu()[rows]
+    short = short_rows(c["cu"])[rows]
+    ref = g[f"{name}|int8_b_qgroup32"]
+    e = O.compare(ref[short], o[short])
+    record("golden_int8_b_qgroup32", case=name, split=split, **e)
+    assert e["rel_l2"] < REL_L2, e
+    strict = O.paged_static_attention(O.CFG32_G32_Q32, c["static"], True, 8)(
+        c["q"].float(), kq, vq, c["cu"], c["seq_lens"], c["block_table"], c["scale"])[rows]
+    check_attention(strict[short], o[short], "qgroup32_vs_fp32q_oracle", case=name, split=split)
+    if (~short).any():
+        assert O.compare(ref[~short], o[~short])["rel_l2"] < 1e-2
+
+
 # ------------------------------------------------------------------ attention: reference test matrix
 SHAPES = [(28, 4, 128), (12, 2, 128), (32, 8, 128), (16, 1, 128), (14, 2, 64), (16, 4, 64)]
 CASES = {"decode": ([1] * 12, [17, 300, 1, 1024, 2047, 64, 129, 900, 3000, 5, 333, 1500]),
@@ -655,6 +691,23 @@ def test_stream_read_probe_reads_every_word_once(nbytes, wg):
     assert got == np.bitwise_xor.reduce(host.numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("rd,wr,wg", [(2 << 20, 1 << 20, 64), (1 << 20, 2 << 20, 7), (4096 * 3, 4096 * 3, 5),
+                                      (32, 16, 1), ((1 << 20) + 32, (1 << 19) + 16, 1000)])
+def test_stream_rw_probe_writes_exactly_its_bytes(rd, wr, wg):
+    """kvq_stream_rw (bench.py's read + write floor, no counterpart in the reference): every 16-byte chunk of
+    the destination is written and nothing past it, whatever the grid and ratio; other ratios are refused."""
+    from kvq import _native
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (rd // 4,), dtype=torch.int32, device=DEV)
+    dst = torch.full((wr // 4 + 64,), 0x5A5A5A5A, dtype=torch.int32, device=DEV)
+    _native.call("kvq_stream_rw", src.data_ptr(), rd, dst.data_ptr(), wr, wg, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    chunks = dst[:wr // 4].view(-1, 4).cpu()
+    assert not (chunks == 0x5A5A5A5A).all(dim=1).any()
+    assert (dst[wr // 4:] == 0x5A5A5A5A).all()
+    with pytest.raises(_native.NativeError, match="ratio|2 : 1"):
+        _native.call("kvq_stream_rw", src.data_ptr(), 48, dst.data_ptr(), 16, 1, torch.cuda.current_stream().cuda_stream)
+
+
 @pytest.mark.parametrize("wg_per_cu", ["1", "2"])
 def test_quant_cache_ring_path_bit_exact(monkeypatch, wg_per_cu):
     """The wavefront-row kernel's token ring (more tokens per wavefront than it keeps in flight at
@@ -670,3 +723,39 @@ def test_quant_cache_ring_path_bit_exact(monkeypatch, wg_per_cu):
     kc_d, vc_d = kv_d.transpose(1, 2).split(128, dim=-1)
     ck.quant_reshape_and_cache(dev(c["key"]), dev(c["value"]), kc_d, vc_d, dev(c["slots"][:n]), dev(c["static"]))
     assert torch.equal(kv_d.cpu(), kv)
+
+
+# ------------------------------------------------------------------ 32-row verification wavefronts
+@pytest.mark.parametrize("shape", [(28, 4, 128, [8, 5, 8, 6]), (32, 4, 128, [5, 8, 3, 8]), (28, 4, 64, [8, 8, 5, 7]),
+                                   (64, 4, 128, [8, 3, 6, 1]), (14, 1, 128, [4, 8, 3, 8])])
+@pytest.mark.parametrize("split", [False, True])
+def test_rows32_kernel_matches_the_16_row_kernel(shape, split):
+    """Batches with more than 32 (token, q head) rows per kv head run 32-row wavefronts on the 32x32 int8
+    MFMA (verify_kernel): the same per-element arithmetic as the 16-row tiles (KVQ_ROWS32=0), so the
+    outputs agree to bf16 rounding, and both match the oracle; G x q_len of 35..512 rows, head_dim 64
+    and 128, with and without split buffers."""
+    hq, hkv, d, q_lens = shape
+    lens = [3000, 700, 64 * 32 + 5, 17]
+    c = synth.paged_case(hq, hkv, q_lens, [max(L, q) for L, q in zip(lens, q_lens)], head_dim=d, seed=hq + d,
+                         params=synth.channel_params(hkv, d))
+    c["static"] = synth.calibration_scales(hkv, d, synth.channel_params(hkv, d))
+    c["scale"] = d ** -0.5
+    kq, vq = int8_cache(c)
+    dd = dev(c)
+    T = dd["q"].shape[0]
+
+    def run():
+        return ck.decode_attention(dd["q"], dev(kq), dev(vq), nan_like(dd["q"]), dd["cu"], dd["seq_lens"],
+                                   dd["block_table"], c["scale"], dd["static"],
+                                   segm=nan_segm(T, hq, 16, d) if split else None, max_query_len=max(q_lens)).cpu()
+    new = run()
+    os.environ["KVQ_ROWS32"] = "0"
+    try:
+        old = run()
+    finally:
+        del os.environ["KVQ_ROWS32"]
+    assert torch.isfinite(new.float()).all()
+    e = O.compare(old, new)
+    record("rows32_vs_rows16", shape=str(shape), split=split, **e)
+    assert e["max_abs"] <= 1e-2 and e["rel_l2"] < 1e-3, e
+    check_attention(oracle_attention(c, kq, vq), new, "rows32_vs_oracle", shape=str(shape), split=split)

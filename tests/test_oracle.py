@@ -124,6 +124,28 @@ def test_oracle_matches_reference_golden(golden, name):
         assert e2["rel_l2"] < 1e-5
 
 
+@pytest.mark.parametrize("name", cases.WITH_QGROUP32)
+def test_oracle_group32_matches_reference_golden(golden, name):
+    """q scales per 32 channels (int8_ref's q_gran "group32", kvq/int8_ref.py:120-129): the oracle's group
+    path against the reference's own output on the same inputs, and the fp32-q variant (the kernel's q
+    contract) within the attention bar of it."""
+    g, _ = golden
+    c = cases.build(name)
+    kq, vq = _quantized(c)
+    args = (c["cu"], c["seq_lens"], c["block_table"])
+    rows = cases.stored_rows(name, c["cu"])
+    ref = g[f"{name}|int8_b_qgroup32"]
+    out = O.paged_static_attention(O.CFG32_G32, c["static"], True, 8)(c["q"], kq, vq, *args, c["scale"])[rows]
+    err = O.compare(ref, out)
+    record("oracle_group32_vs_reference_golden", case=name, **err)
+    assert err["max_abs"] <= 2 ** -8 * ref.float().abs().max().item() and err["rel_l2"] < 1e-5
+    out32 = O.paged_static_attention(O.CFG32_G32_Q32, c["static"], True, 8)(c["q"], kq, vq, *args, c["scale"])[rows]
+    e32 = O.compare(ref, out32)
+    assert e32["max_abs"] <= 2e-2 and e32["mean_abs"] <= 2e-3, e32
+    # groups change the numbers: the per-row fixture differs from the per-group one
+    assert O.compare(g[f"{name}|int8_b"], ref)["max_abs"] > 0
+
+
 # ---------------------------------------------------------------- invariants of implementation B
 def _dense_case(b=2, R=3, K=70, hkv=2, G=3, D=64, seed=0):
     gen = torch.Generator().manual_seed(seed)

@@ -79,14 +79,16 @@ def test_plugin_installs_capture(monkeypatch):
 
 
 # ------------------------------------------------------------------ impl
-@pytest.mark.parametrize("cfg", ["B_channel_smooth", "B_channel", "B_head_smooth", "B_head"])
+@pytest.mark.parametrize("cfg", ["B_channel_smooth", "B_channel", "B_head_smooth", "B_head", "B_channel_qgroup32",
+                                 "B_channel_smooth_qgroup32"])
 def test_impl_accepts_the_kernel_configs(cfg, monkeypatch):
     impl = _impl(cfg=cfg, monkeypatch=monkeypatch)
     assert impl.cfg_name == cfg and impl.kv_cache_dtype == "int8_static"
     assert impl.fused_output_quant_supported(None) is False
+    assert impl.q_group == (32 if cfg.endswith("qgroup32") else None)
 
 
-@pytest.mark.parametrize("cfg", ["A_channel", "B_channel_pnone", "B_channel_qgroup32", "B_channel_qtensor"])
+@pytest.mark.parametrize("cfg", ["A_channel", "B_channel_pnone", "B_channel_qtensor", "B_channel_smooth_qnone"])
 def test_impl_rejects_configs_the_kernels_do_not_compute(cfg, monkeypatch):
     with pytest.raises(AssertionError, match="implement B"):
         _impl(cfg=cfg, monkeypatch=monkeypatch)
