@@ -1861,10 +1861,9 @@ __global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs
 }
 
 // ------------------------------------------------------------------------------------------------
-// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542). One wavefront
-// per (output page, head), the 4 wavefronts of a workgroup on consecutive heads of one page (so a
-// workgroup reads and writes contiguous runs); a lane converts 16 channels of one (token, head): a
-// 16-byte int8 load, two 16-byte bf16 stores (v_cvt_pk_bf16_f32, round to nearest even).
+// Page dequantization for the long-query path (reference kvq/cuda/int8_kv.cu:505-542): a lane converts
+// 16 channels of one (token, head) -- a 16-byte int8 load, two 16-byte bf16 stores (bf16_rne(f32(code) *
+// scale), v_cvt_pk_bf16_f32, round to nearest even).
 // ------------------------------------------------------------------------------------------------
 __device__ __forceinline__ float i8f(uint32_t w, int b) { return (float)(int8_t)(w >> (8 * b)); }
 
@@ -1884,51 +1883,69 @@ __device__ __forceinline__ u32x4 dq8(uint32_t w0, uint32_t w1, const float* s) {
   return o;
 }
 
+// 8 codes (two dwords) -> 8 bf16 (one 16-byte store)
+__device__ __forceinline__ u32x4 dq8x(uint32_t w0, uint32_t w1, const float (&s)[8]) {
+  const float tmp[8] = {s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]};
+  return dq8(w0, w1, tmp);
+}
+
+// One workgroup per output page (blockIdx.x) and group of heads (blockIdx.y): its page id chain (src_req,
+// src_j, block table) is read once, by scalar loads. Thread tid owns combination k = tid % C of (head,
+// K|V, 8-channel chunk) -- C = heads * 2 * D / 8 of them, chunks fastest -- and tokens tid / C, + TPC, ...
+// of the page (TPC = threads / C), its 8 scales in registers; up to DQ_BATCH 8-byte code loads are in
+// flight before they are converted and stored. A lane's 8 bf16 are one 16-byte store and consecutive
+// lanes' stores are consecutive: each store instruction writes whole rows of the output [P, bs, H, D]
+// (16 lanes per 256-byte K or V row at D = 128), never parts of lines.
+constexpr int DQ_BATCH = 16;
 template <int D>
 __global__ __launch_bounds__(256) void dequant_pages_kernel(
     const int8_t* __restrict__ kc, int64_t k_sb, int64_t k_sn, int64_t k_sh, const int8_t* __restrict__ vc,
-    int64_t v_sb, int64_t v_sn, int64_t v_sh, int num_blocks, int bs, int H, uint16_t* __restrict__ ko,
-    uint16_t* __restrict__ vo, const int* __restrict__ bt, int64_t bt_stride, const int* __restrict__ src_req,
-    const int* __restrict__ src_j, int P, const float* __restrict__ ks, int ks_pc, const float* __restrict__ vs,
-    int vs_pc) {
-  // One wavefront per (output page, head). A token's K and V rows are 2 * D / 16 lanes' worth of
-  // 16-byte runs; lane l keeps the same run position (K or V, channels) for every token it visits,
-  // so its 16 scales are loaded once. All of the lane's loads for the page are issued before any
-  // conversion.
-  constexpr int CPL = 16, RUNS = 2 * D / CPL;   // 16-channel runs per token (K then V)
-  constexpr int TPW = WAVE / RUNS;              // tokens per wavefront pass
-  constexpr int MAXP = 8;                       // passes in flight: block sizes up to TPW * MAXP
-  const int lane = threadIdx.x & (WAVE - 1);
-  const int unit = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
-  if (unit >= P * H) return;
-  const int p = unit / H, h = unit % H;
-  const int run = lane % RUNS, t0 = lane / RUNS;
-  const bool is_v = run >= RUNS / 2;
-  const int d0 = (run % (RUNS / 2)) * CPL;
-  float sc[CPL];
-  const float* sp = is_v ? vs : ks;
-  const int pc = is_v ? vs_pc : ks_pc;
-#pragma unroll
-  for (int e = 0; e < CPL; ++e) sc[e] = sp[pc ? h * D + d0 + e : h];
-  int src = bt[(int64_t)src_req[p] * bt_stride + src_j[p]];
+    int64_t v_sb, int64_t v_sn, int64_t v_sh, int num_blocks, int bs, int H, int heads_per_block,
+    uint16_t* __restrict__ ko, uint16_t* __restrict__ vo, const int* __restrict__ bt, int64_t bt_stride,
+    const int* __restrict__ src_req, const int* __restrict__ src_j, const float* __restrict__ ks, int ks_pc,
+    const float* __restrict__ vs, int vs_pc) {
+  constexpr int CPK = D / 8;                      // 8-channel chunks of one K (or V) row
+  constexpr int CPH = 2 * CPK;                    // combinations per head: K and V chunks
+  const int p = blockIdx.x;
+  const int h0 = blockIdx.y * heads_per_block;
+  const int nh = min(heads_per_block, H - h0);
+  const int C = nh * CPH;
+  const int tpc = blockDim.x / C;                 // threads per combination (token slices)
+  const int tid = threadIdx.x;
+  if (tid >= C * tpc) return;
+  const int k = tid % C, t0 = tid / C;
+  const int h = h0 + k / CPH, kv = (k % CPH) / CPK, d0 = 8 * (k % CPK);
+  // page id: three dependent loads, uniform across the workgroup (scalar)
+  const int r = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)src_req)[p]);
+  const int j = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)src_j)[p]);
+  int src = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[(int64_t)r * bt_stride + j]);
   if (src < 0 || src >= num_blocks) src = 0;
-  const int8_t* base = (is_v ? vc + (int64_t)src * v_sb + (int64_t)h * v_sh : kc + (int64_t)src * k_sb + (int64_t)h * k_sh) + d0;
-  const int64_t tstride = is_v ? v_sn : k_sn;
-  uint16_t* obase = (is_v ? vo : ko) + ((int64_t)p * bs * H + h) * D + d0;
-  for (int tb = 0; tb < bs; tb += TPW * MAXP) {
-    u32x4 w[MAXP];
+  float sc[8];
+  const float* sp = kv ? vs : ks;
+  if (kv ? vs_pc : ks_pc) {
+    const float4 f0 = *reinterpret_cast<const float4*>(sp + h * D + d0);
+    const float4 f1 = *reinterpret_cast<const float4*>(sp + h * D + d0 + 4);
+    sc[0] = f0.x; sc[1] = f0.y; sc[2] = f0.z; sc[3] = f0.w; sc[4] = f1.x; sc[5] = f1.y; sc[6] = f1.z; sc[7] = f1.w;
+  } else {
+    const float v = sp[h];
 #pragma unroll
-    for (int i = 0; i < MAXP; ++i) {
-      const int tkn = tb + t0 + i * TPW;
-      if (tkn < bs) w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + tkn * tstride));
+    for (int e = 0; e < 8; ++e) sc[e] = v;
+  }
+  const int8_t* base = kv ? vc + (int64_t)src * v_sb + (int64_t)h * v_sh + d0 : kc + (int64_t)src * k_sb + (int64_t)h * k_sh + d0;
+  const int64_t tstride = kv ? v_sn : k_sn;
+  uint16_t* obase = (kv ? vo : ko) + ((int64_t)p * bs * H + h) * D + d0;
+  for (int tb = t0; tb < bs; tb += DQ_BATCH * tpc) {
+    u32x2 w[DQ_BATCH];
+#pragma unroll
+    for (int i = 0; i < DQ_BATCH; ++i) {
+      const int t = tb + i * tpc;
+      if (t < bs) w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(base + t * tstride));
     }
 #pragma unroll
-    for (int i = 0; i < MAXP; ++i) {
-      const int tkn = tb + t0 + i * TPW;
-      if (tkn >= bs) break;
-      u32x4* o = reinterpret_cast<u32x4*>(obase + (int64_t)tkn * H * D);
-      __builtin_nontemporal_store(dq8(w[i].x, w[i].y, sc), o);
-      __builtin_nontemporal_store(dq8(w[i].z, w[i].w, sc + 8), o + 1);
+    for (int i = 0; i < DQ_BATCH; ++i) {
+      const int t = tb + i * tpc;
+      if (t >= bs) break;
+      __builtin_nontemporal_store(dq8x(w[i].x, w[i].y, sc), reinterpret_cast<u32x4*>(obase + (int64_t)t * H * D));
     }
   }
 }
@@ -2986,16 +3003,23 @@ int kvq_dequant_pages(const int8_t* k_cache, int64_t k_sb, int64_t k_sn, int64_t
   if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(k_out) || !aligned16(v_out) ||
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 16)
     return fail("dequant_pages: rows must be 16-byte aligned (base pointers and strides)");
+  if ((k_scale_cols > 1 && !aligned16(k_scale)) || (v_scale_cols > 1 && !aligned16(v_scale)))
+    return fail("dequant_pages: per-channel scale tables must be 16-byte aligned");
   if (num_pages > INT32_MAX || num_blocks > INT32_MAX) return fail("dequant_pages: too many pages");
-  if (num_pages * num_heads > (int64_t)INT32_MAX * 4 / 5) return fail("dequant_pages: too many pages");
-  const int64_t units = num_pages * num_heads;
+  if (num_heads > 65535 * 4) return fail("dequant_pages: too many heads");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int grid = (int)((units + 3) / 4);
+  // heads per workgroup: as many as 256 threads' worth of (head, K|V, chunk) combinations; threads: the
+  // largest multiple of those combinations up to 256
+  const int cph = 2 * (int)head_dim / 8;
+  const int hpb = (int)std::min<int64_t>(num_heads, 256 / cph);
+  const int combos = hpb * cph;
+  const int threads = (256 / combos) * combos;
+  const dim3 grid((unsigned)num_pages, (unsigned)((num_heads + hpb - 1) / hpb));
   auto go = [&](auto kern) {
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(4 * WAVE), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,
-                       (int)num_blocks, (int)block_size, (int)num_heads, (uint16_t*)k_out, (uint16_t*)v_out,
-                       block_table, bt_stride, src_req, src_j, (int)num_pages, k_scale, (int)(k_scale_cols > 1),
-                       v_scale, (int)(v_scale_cols > 1));
+    hipLaunchKernelGGL(kern, grid, dim3(threads), 0, st, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh,
+                       (int)num_blocks, (int)block_size, (int)num_heads, hpb, (uint16_t*)k_out, (uint16_t*)v_out,
+                       block_table, bt_stride, src_req, src_j, k_scale, (int)(k_scale_cols > 1), v_scale,
+                       (int)(v_scale_cols > 1));
   };
   if (head_dim == 128) go(dequant_pages_kernel<128>);
   else go(dequant_pages_kernel<64>);

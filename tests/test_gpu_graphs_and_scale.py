@@ -1,6 +1,7 @@
 """HIP-graph capture (the reference's tests/test_cudagraph.py) and parity at the benchmark sizes
 (configs c2, c3, c4 of BASELINE.json), through size-independent checks: sampled requests against the
 CPU oracle, split-count invariance, and the bit-exact cache codes of the GPU fill."""
+import math
 import os
 
 import pytest
@@ -209,3 +210,52 @@ def test_c4_decode_rows_sampled_parity(split):
         err = O.compare(ref, out[r:r + 1].cpu())
         record("c4_sampled", request=r, L=lens[r], split=split, **err)
         assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (r, lens[r], err)
+
+
+def test_c4_full_batch_in_one_paged_attention_call():
+    """c4 as one step: 96 decode rows (L log-uniform in [1, 32768]) and 4 prefill requests of 16384 tokens
+    in a single paged_attention call (plan_long for the long requests, no split buffers: 65,632 tokens,
+    the one-pass INT8 path), Llama-3 heads 32 / 8. Sampled decode rows against the oracle, sampled
+    prefill rows against fp32 attention over the dequantized pages."""
+    dec = synth.c4_lens()
+    hq, hkv, d, bs = 32, 8, 128, 16
+    Q = 16384
+    lens = dec + [Q] * 4
+    q_lens = [1] * len(dec) + [Q] * 4
+    pages = [-(-L // bs) for L in lens]
+    nb = sum(pages) + 64
+    params = synth.channel_params(hkv, d)
+    st = {k: v.to(DEV) for k, v in synth.calibration_scales(hkv, d, params).items()}
+    kv, kc, vc = _interleaved(nb, hkv, bs, d)
+    synth.fill_cache_gpu(kc, vc, st, params, seed=70, write=ck.quant_reshape_and_cache)
+    bt = synth.random_block_table(len(lens), pages, nb, 71, DEV)
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(q_lens), 0).tolist()), dtype=torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    g = torch.Generator(device=DEV).manual_seed(72)
+    T = int(cu[-1])
+    q = torch.randn(T, hq, d, generator=g, device=DEV).to(torch.bfloat16)
+    plan = ck.plan_long(cu, sl, bs)
+    assert plan is not None and plan.has_short and plan.src_req.shape[0] == 4 * (Q // bs)
+    out = ck.paged_attention(q, kc, vc, nan_like(q), cu.to(DEV), sl.to(DEV), bt, Q, SCALE, st, plan)
+    torch.cuda.synchronize()
+    order = sorted(range(len(dec)), key=lambda r: dec[r])
+    for r in [order[0], order[1], order[47], order[-2], order[-1]] + order[5::20]:
+        ref = _request_oracle(kc, vc, bt, r, lens[r], q[int(cu[r]):int(cu[r]) + 1], st)
+        err = O.compare(ref, out[int(cu[r]):int(cu[r]) + 1].cpu())
+        record("c4_one_call_decode", request=r, L=lens[r], **err)
+        assert err["max_abs"] <= 2e-2 and err["mean_abs"] <= 2e-3, (r, lens[r], err)
+    rng = synth.rng(73)
+    for r in range(len(dec), len(lens)):
+        ids = bt[r, :pages[r]].long()
+        k = (kc[ids].float() * st["k_scale"]).to(torch.bfloat16).float().reshape(Q, hkv, d)   # dequant_pages
+        v = (vc[ids].float() * st["v_scale"]).to(torch.bfloat16).float().reshape(Q, hkv, d)
+        kT = k.repeat_interleave(hq // hkv, dim=1).permute(1, 2, 0).contiguous()
+        vv = v.repeat_interleave(hq // hkv, dim=1).permute(1, 0, 2).contiguous()
+        for t in sorted({0, Q - 1} | set(int(x) for x in rng.integers(0, Q, 6))):
+            qi = q[int(cu[r]) + t].float()[:, None, :].contiguous()
+            sc = torch.matmul(qi, kT) / math.sqrt(d)
+            sc[:, :, t + 1:] = float("-inf")
+            o = torch.matmul(torch.softmax(sc, dim=-1), vv).squeeze(1)
+            err = O.compare(o.cpu(), out[int(cu[r]) + t].float().cpu())
+            record("c4_one_call_prefill", request=r, row=t, **err)
+            assert err["max_abs"] <= 2e-2 and err["rel_l2"] < 1e-2, (r, t, err)
