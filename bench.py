@@ -4,9 +4,10 @@
 Headline (BASELINE.json metric, config c2): INT8 paged decode attention, 128 requests x 32768 keys,
 28 q / 4 kv heads, head_dim 128, block 16, in vLLM's interleaved [nb, H, bs, 2D] int8 cache (filled
 with c0-distribution codes by this package's quantize-and-cache kernel), shuffled block tables over
-263,168 blocks. A step is one kvq.cuda_kernels.decode_attention call (attention kernel + split merge)
-with split buffers allocated once beforehand, as the vLLM backend passes its metadata's, and every input
-resident in HBM. The same call without split buffers (one pass, nothing allocated) is reported beside it.
+263,168 blocks. A step is one kvq.cuda_kernels.decode_attention call made as the vLLM backend makes it
+for this batch -- 128 requests are more than vLLM's split buffers serve (128 // 4 kv heads), so none are
+passed: one pass, nothing allocated -- with every input resident in HBM. The same call with split
+buffers allocated once beforehand (attention kernel + split merge) is reported beside it.
 
 Prints ONE JSON line. `value` is algorithmic bytes / step time (GB/s); `roofline` times the attention
 kernel alone with HIP events recorded around it on its own stream; `cpu_baseline` times the CPU oracle
@@ -88,6 +89,17 @@ def build_c2(B=128, L=32768, hq=28, hkv=4, d=128, bs=16):
     alg = (B * L * hkv * d * 2 + 2 * B * hq * d * 2 + B * pages * 4 + (2 * B + 1) * 4 + 2 * hkv * d * 4)
     return {"q": q, "kc": kc, "vc": vc, "kv": kv, "cu": cu, "sl": sl, "bt": bt, "st": st, "B": B, "L": L,
             "hq": hq, "hkv": hkv, "d": d, "bs": bs, "alg_bytes": alg, "kv_bytes": B * L * hkv * d * 2}
+
+
+MIN_LAUNCH_GRID_SIZE_2D = 128   # vLLM's Triton builder: split buffers for up to 128 // kv heads requests
+
+
+def backend_passes_split_buffers(num_reqs, num_tokens, num_kv_heads):
+    """Whether the vLLM backend hands the kernel vLLM's split buffers for this batch (kvq.vllm_int8.backend
+    Int8StaticImpl._split_buffers, reference backend.py:175-177): vLLM's Triton metadata holds them for
+    batches of up to 128 // kv heads requests, with that many rows."""
+    threshold = MIN_LAUNCH_GRID_SIZE_2D // num_kv_heads
+    return num_reqs <= threshold and num_tokens <= threshold
 
 
 def time_c2(w, steps, warmup, split=True):
@@ -323,17 +335,32 @@ def bench_c1(reps=20):
         ck.quant_reshape_and_cache(k, v, kc, vc, sl, st)
 
     ms = _median_event_ms(fn, reps, len(sets))
+
+    # the floor: the same bytes read and scattered by slot into the same caches, without the arithmetic
+    def scatter(i):
+        k, v, kc, vc, sl, st = sets[i]
+        _native.call("kvq_stream_scatter", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0),
+                     v.stride(1), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), sl.data_ptr(),
+                     sl.shape[0], kc.shape[2], kc.shape[3], kc.shape[0], kc.shape[1],
+                     torch.cuda.current_stream().cuda_stream)
+
+    ms_sc = _median_event_ms(scatter, reps, len(sets))
     del sets
-    # the floor: a plain in-order stream of the same bytes (K/V rows read, codes written)
+    # and a plain in-order stream of those bytes (no scatter)
     f_us, f_wg = rw_floor(t_valid * 2048, t_valid * 1024)
+    sc_alg = t_valid * 3072
     return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
             "alg_bytes": alg, "tokens": T, "valid": t_valid,
-            "ceiling": {"us": round(f_us, 2), "GBps": round((t_valid * 3072) / f_us / 1e3, 1),
-                        "frac_of_peak": round((t_valid * 3072) / f_us / 1e3 / PEAK_GBS, 4),
-                        "kernel_vs_ceiling": round(ms * 1e3 / f_us, 3),
-                        "how": "kvq_stream_rw: %d B read + %d B written in order (c1's K/V rows and codes, no slot "
-                               "scatter, no arithmetic), %d workgroups per CU, same graph replay and rotation"
-                               % (t_valid * 2048, t_valid * 1024, f_wg)}}
+            "ceiling": {"us": round(ms_sc * 1e3, 2), "GBps": round(sc_alg / ms_sc / 1e6, 1),
+                        "frac_of_peak": round(sc_alg / ms_sc / 1e6 / PEAK_GBS, 4),
+                        "kernel_vs_ceiling": round(ms / ms_sc, 3),
+                        "how": "kvq_stream_scatter: c1's K/V rows read and one byte per element written through "
+                               "slot_mapping into the same interleaved caches (the write's traffic and scatter, no "
+                               "arithmetic), same graph replay and rotation"},
+            "ceiling_linear": {"us": round(f_us, 2), "GBps": round(sc_alg / f_us / 1e3, 1),
+                               "kernel_vs_ceiling": round(ms * 1e3 / f_us, 3),
+                               "how": "kvq_stream_rw: %d B read + %d B written in order (no scatter), %d workgroups "
+                                      "per CU" % (t_valid * 2048, t_valid * 1024, f_wg)}}
 
 
 def bench_c3(reps=20, one_pass=True):
@@ -479,7 +506,10 @@ def main():
     w = build_c2()
     torch.cuda.synchronize()
     print("# timing c2", file=sys.stderr, flush=True)
-    out, ms_step, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup)
+    # the call as the vLLM backend makes it for this batch: 128 requests > 128 // 4 kv heads, so no split
+    # buffers (one pass); the call with split buffers is reported beside it
+    split = backend_passes_split_buffers(w["B"], w["B"], w["hkv"])
+    out, ms_step, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup, split=split)
     alg = w["alg_bytes"]
     res = {
         "metric": METRIC,
@@ -494,19 +524,23 @@ def main():
         "data": "synthetic (c0 distribution, seeded)",
         "config": {"workload": "c2: INT8 paged decode attention, 128 requests x 32768 keys, 28 q / 4 kv heads, "
                                "d128, block 16, vLLM interleaved int8 cache, shuffled block tables",
-                   "max_splits": splits, "parallelism": "single GPU"},
+                   "split_buffers": split, "max_splits": splits,
+                   "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch (no split "
+                           "buffers above 128 // kv heads requests: one pass, nothing allocated)" if not split else
+                           "kvq.cuda_kernels.decode_attention with split buffers",
+                   "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / (kern_ms_mean * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(alg / (kern_ms_mean * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
                      "kernel": "attn_kernel<128,3>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
-    _, ms1, k1_mean, _, _ = time_c2(w, max(5, args.steps // 2), 2, split=False)
-    res["c2_one_pass"] = {"what": "the same call without split buffers: one pass, each (request, kv head) whole in "
-                                  "one workgroup, nothing allocated (what the vLLM backend runs when num_reqs > "
-                                  "seq_threshold_3D)",
-                          "us_per_call": round(ms1 * 1e3, 1), "kernel_us_mean": round(k1_mean * 1e3, 1),
-                          "GBps": round(alg / (ms1 * 1e-3) / 1e9, 1),
-                          "frac": round(alg / (ms1 * 1e-3) / 1e9 / PEAK_GBS, 4)}
+    _, ms1, k1_mean, _, s1 = time_c2(w, max(5, args.steps // 2), 2, split=not split)
+    res["c2_other_call"] = {
+        "what": ("with split buffers allocated once beforehand (%d pieces per row at most): segments cut across "
+                 "workgroups, fp32 partials merged by split_reduce_kernel" % s1) if not split else
+                "without split buffers: one pass, each (request, kv head) whole in one workgroup",
+        "us_per_call": round(ms1 * 1e3, 1), "kernel_us_mean": round(k1_mean * 1e3, 1),
+        "GBps": round(alg / (ms1 * 1e-3) / 1e9, 1), "frac": round(alg / (ms1 * 1e-3) / 1e9 / PEAK_GBS, 4)}
     ceil_gbs, ceil_wg = read_ceiling(w["kv"])
     res["roofline"]["read_ceiling"] = {
         "GBps": round(ceil_gbs, 1), "frac_of_peak": round(ceil_gbs / PEAK_GBS, 4),

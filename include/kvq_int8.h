@@ -190,6 +190,17 @@ int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t work
 int kvq_stream_rw(const void* src, int64_t read_bytes, void* dst, int64_t write_bytes, int64_t workgroups,
                   void* stream);
 
+/* Instrumentation, no counterpart in the reference: the memory traffic of kvq_quant_cache without its
+ * arithmetic. Reads the key and value rows [T, H, D] bf16 (heads contiguous) of the tokens whose slot is
+ * in [0, num_blocks * block_size) and writes one byte per element (the bf16's high byte) to both caches'
+ * rows (slot / block_size, slot % block_size, head) -- caches of strides c_sb, c_sn, c_sh bytes (the K
+ * and V views of one layout share them). Timed beside kvq_quant_cache it gives the floor of a stream of
+ * those bytes scattered by slot. Stream-ordered, allocates nothing. */
+int kvq_stream_scatter(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
+                       int64_t val_sh, int8_t* k_cache, int8_t* v_cache, int64_t c_sb, int64_t c_sn, int64_t c_sh,
+                       const int64_t* slot_mapping, int64_t n_tokens, int64_t num_heads, int64_t head_dim,
+                       int64_t num_blocks, int64_t block_size, void* stream);
+
 /* Text of the last error on this thread ("" if none). */
 const char* kvq_last_error(void);
 

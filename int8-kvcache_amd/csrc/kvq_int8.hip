@@ -29,6 +29,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <string>
@@ -2465,6 +2466,44 @@ __global__ __launch_bounds__(256) void stream_rw_kernel(const u32x4* __restrict_
   }
 }
 
+// Streaming scatter probe, no counterpart in the reference: the cache write's memory traffic without
+// its arithmetic. For tokens t < n whose slot >= 0, each lane reads a 16-byte piece (8 bf16 channels) of
+// key row t and of value row t and writes one byte per channel (the bf16's high byte, a byte shuffle)
+// to cache row (slot / bs, slot % bs, head) of kc and vc -- the same bytes, addresses and scatter by slot
+// as the fused quantize + cache write. Consecutive lanes take consecutive pieces of a row (16-byte
+// loads contiguous across the wavefront, 8-byte stores filling whole 128-byte cache rows) and each lane
+// keeps SC_TPL tokens in flight; the grid covers n_tokens * pieces lanes.
+constexpr int SC_TPL = 4;
+__global__ __launch_bounds__(256) void stream_scatter_kernel(
+    const uint16_t* __restrict__ key, int64_t key_st, const uint16_t* __restrict__ value, int64_t val_st,
+    int8_t* __restrict__ kc, int8_t* __restrict__ vc, int64_t sb, int64_t sn, int64_t sh, int pieces_per_head,
+    int pieces, const int64_t* __restrict__ slots, int n_tokens, int lbs, int64_t num_slots) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = (int)(gid % pieces);
+  const int64_t t0 = gid / pieces * SC_TPL;
+  const int h = c / pieces_per_head, cc = c % pieces_per_head;
+  u32x4 kw[SC_TPL], vw[SC_TPL];
+  int64_t sl[SC_TPL];
+#pragma unroll
+  for (int i = 0; i < SC_TPL; ++i) {
+    const int64_t t = t0 + i;
+    sl[i] = t < n_tokens ? slots[t] : -1;
+    if (t < n_tokens) {
+      kw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(key + t * key_st) + c);
+      vw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(value + t * val_st) + c);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < SC_TPL; ++i) {
+    if (sl[i] < 0 || sl[i] >= num_slots) continue;
+    const int64_t off = (sl[i] >> lbs) * sb + (sl[i] & ((1 << lbs) - 1)) * sn + (int64_t)h * sh + 8 * cc;
+    const u32x2 kb{__builtin_amdgcn_perm(kw[i].y, kw[i].x, 0x07050301u), __builtin_amdgcn_perm(kw[i].w, kw[i].z, 0x07050301u)};
+    const u32x2 vb{__builtin_amdgcn_perm(vw[i].y, vw[i].x, 0x07050301u), __builtin_amdgcn_perm(vw[i].w, vw[i].z, 0x07050301u)};
+    __builtin_nontemporal_store(kb, reinterpret_cast<u32x2*>(kc + off));
+    __builtin_nontemporal_store(vb, reinterpret_cast<u32x2*>(vc + off));
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Host side: argument checks, launches, error reporting.
 // ------------------------------------------------------------------------------------------------
@@ -2705,7 +2744,28 @@ int kvq_stream_rw(const void* src, int64_t read_bytes, void* dst, int64_t write_
   return launched("stream_rw");
 }
 
-int kvq_abi_version(void) { return 7; }
+int kvq_stream_scatter(const void* key, int64_t key_st, int64_t key_sh, const void* value, int64_t val_st,
+                       int64_t val_sh, int8_t* k_cache, int8_t* v_cache, int64_t c_sb, int64_t c_sn, int64_t c_sh,
+                       const int64_t* slot_mapping, int64_t n_tokens, int64_t num_heads, int64_t head_dim,
+                       int64_t num_blocks, int64_t block_size, void* stream) {
+  if (head_dim != 64 && head_dim != 128) return fail("stream_scatter: head_dim must be 64 or 128");
+  if (n_tokens < 0 || n_tokens > INT32_MAX || num_heads <= 0 || !pow2(block_size)) return fail("stream_scatter: bad sizes");
+  if (n_tokens == 0) { g_err.clear(); return KVQ_OK; }
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping) return fail("stream_scatter: null pointer");
+  if (key_sh != head_dim || val_sh != head_dim || !aligned16(key) || !aligned16(value) || (key_st | val_st) % 8 ||
+      ((uintptr_t)k_cache | (uintptr_t)v_cache | c_sb | c_sn | c_sh) % 8)
+    return fail("stream_scatter: key / value rows [T, H, D] with contiguous heads, 16-byte aligned; 8-byte aligned caches");
+  const int pph = (int)(head_dim / 8), pieces = (int)(num_heads * pph);
+  const int64_t lanes = (n_tokens + SC_TPL - 1) / SC_TPL * pieces;
+  if (lanes / 256 + 1 > INT32_MAX) return fail("stream_scatter: too many tokens");
+  hipLaunchKernelGGL(stream_scatter_kernel, dim3((unsigned)((lanes + 255) / 256)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), (const uint16_t*)key, key_st, (const uint16_t*)value, val_st,
+                     k_cache, v_cache, c_sb, c_sn, c_sh, pph, pieces, slot_mapping, (int)n_tokens, log2i(block_size),
+                     num_blocks * block_size);
+  return launched("stream_scatter");
+}
+
+int kvq_abi_version(void) { return 8; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 
@@ -2737,7 +2797,10 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
   const int64_t key_bytes = 2 * ((n_tokens - 1) * key_st + (num_heads - 1) * key_sh + head_dim);
   const int64_t val_bytes = 2 * ((n_tokens - 1) * val_st + (num_heads - 1) * val_sh + head_dim);
   const int64_t row_bytes = (num_heads - 1) * std::max(kc_sh, vc_sh) + head_dim;
-  if ((num_heads * head_dim) % (WAVE * QC_CPL) == 0 && std::max({key_bytes, val_bytes, row_bytes}) <= INT32_MAX) {
+  // KVQ_QC_KERNEL=lanes: the lane kernel wherever a token's lanes fit one workgroup (a test knob)
+  const char* qk = getenv("KVQ_QC_KERNEL");
+  const bool lanes_only = qk && strcmp(qk, "lanes") == 0 && num_heads * (head_dim / QC_CPL) <= QC_BLOCK;
+  if (!lanes_only && (num_heads * head_dim) % (WAVE * QC_CPL) == 0 && std::max({key_bytes, val_bytes, row_bytes}) <= INT32_MAX) {
     // whole wavefronts per token: the wavefront-row kernel; the grid holds a whole number of tokens'
     // wavefronts (wpt) and no more workgroups than are resident at once
     // a workgroup owns one of the token's wpt parts for QC_BLOCK / WAVE tokens at a time (the grid

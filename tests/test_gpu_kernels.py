@@ -63,9 +63,17 @@ def short_rows(cu, limit=ck.SHORT_Q):
 
 
 # ------------------------------------------------------------------ quant + cache write
+@pytest.fixture(params=["rows", "lanes"])
+def qc_kernel(request, monkeypatch):
+    """The fused cache write's two kernels (KVQ_QC_KERNEL): the wavefront-row kernel (the default where
+    a token's channels are whole wavefronts; other shapes take the lane kernel) and the lane kernel."""
+    monkeypatch.setenv("KVQ_QC_KERNEL", request.param)
+    return request.param
+
+
 @pytest.mark.parametrize("D", [128, 64])
 @pytest.mark.parametrize("per_channel", [True, False])
-def test_quant_cache_matches_oracle(per_channel, D):
+def test_quant_cache_matches_oracle(per_channel, D, qc_kernel):
     """tests/test_cuda_kernels.py:26-43 of the reference: vLLM's [nb, H, bs, 2D] layout, 8 padded key
     rows, every 17th slot -1, keys x5; codes bit-exact."""
     r = synth.rng(0)
@@ -86,7 +94,7 @@ def test_quant_cache_matches_oracle(per_channel, D):
 
 @pytest.mark.parametrize("H,D", [(8, 128), (12, 128), (32, 128), (16, 64), (2, 128), (1, 64)])
 @pytest.mark.parametrize("layout", ["interleaved", "separate"])
-def test_quant_cache_head_counts_and_packed_qkv(H, D, layout):
+def test_quant_cache_head_counts_and_packed_qkv(H, D, layout, qc_kernel):
     """Head counts whose channels fill 1, 2, 3 or 8 wavefronts per token (the wavefront-row kernel)
     and fewer than one (the lane kernel); K/V are strided views of a packed qkv activation
     [T, Hq + 2H, D], the cache vLLM's interleaved [nb, H, bs, 2D] or two separate [nb, bs, H, D]
@@ -114,7 +122,7 @@ def test_quant_cache_head_counts_and_packed_qkv(H, D, layout):
     assert torch.equal(kc_d.cpu(), kc) and torch.equal(vc_d.cpu(), vc)
 
 
-def test_quant_cache_c1_full_size_bit_exact():
+def test_quant_cache_c1_full_size_bit_exact(qc_kernel):
     """BASELINE config c1: 16384 tokens x 4 x 128, ~2% padded slots, 4096 x 16 interleaved cache."""
     c = synth.c1_inputs()
     nb, bs = c["num_blocks"], c["block_size"]
@@ -132,7 +140,7 @@ def test_quant_cache_c1_full_size_bit_exact():
     assert torch.equal(kc[s // bs, s % bs], rows)
 
 
-def test_quant_cache_rounding_boundaries():
+def test_quant_cache_rounding_boundaries(qc_kernel):
     """Quotients on and within a few ulp of half-integers (the kernel's exact-division slow path),
     and saturation: bit-exact against the IEEE C restatement."""
     r = synth.rng(2)
@@ -597,7 +605,7 @@ def test_key_split_workgroups_agree(q_len, segm):
 # ------------------------------------------------------------------ block sizes beyond 16
 @pytest.mark.parametrize("bs", [32, 64])
 @pytest.mark.parametrize("H,D", [(4, 128), (2, 64), (3, 128)])
-def test_quant_cache_block_sizes(bs, H, D):
+def test_quant_cache_block_sizes(bs, H, D, qc_kernel):
     """Cache blocks of 32 and 64 slots (vLLM's other block sizes), interleaved layout; both kernels
     (H x D a multiple of 512 or not); codes bit-exact."""
     r = synth.rng(bs * 100 + H * 10 + D)
@@ -706,6 +714,30 @@ def test_stream_rw_probe_writes_exactly_its_bytes(rd, wr, wg):
     assert (dst[wr // 4:] == 0x5A5A5A5A).all()
     with pytest.raises(_native.NativeError, match="ratio|2 : 1"):
         _native.call("kvq_stream_rw", src.data_ptr(), 48, dst.data_ptr(), 16, 1, torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("H,D", [(4, 128), (2, 64), (3, 128)])
+def test_stream_scatter_probe_writes_the_cache_writes_bytes(H, D):
+    """kvq_stream_scatter (bench.py's cache-write floor, no counterpart in the reference): exactly the cache
+    rows the fused write fills (valid slots of the interleaved layout), each byte the bf16's high byte."""
+    from kvq import _native
+    r = synth.rng(H * 1000 + D)
+    T, nb, bs = 301, 40, 16
+    key = torch.from_numpy(r.integers(-2 ** 15, 2 ** 15, (T, H, D)).astype(np.int16)).to(DEV)
+    value = torch.from_numpy(r.integers(-2 ** 15, 2 ** 15, (T, H, D)).astype(np.int16)).to(DEV)
+    slots = torch.from_numpy(r.permutation(nb * bs)[:T].astype(np.int64))
+    slots[::7] = -1
+    kv = torch.zeros(nb, H, bs, 2 * D, dtype=torch.int8, device=DEV)
+    kc, vc = kv.transpose(1, 2).split(D, dim=-1)
+    _native.call("kvq_stream_scatter", key.data_ptr(), key.stride(0), key.stride(1), value.data_ptr(), value.stride(0),
+                 value.stride(1), kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2),
+                 slots.to(DEV).data_ptr(), T, H, D, nb, bs, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    want = torch.zeros(nb, bs, H, 2 * D, dtype=torch.int8)
+    ok = slots >= 0
+    hi = lambda x: (x.cpu()[ok].view(torch.uint8).reshape(-1, H, D, 2)[..., 1]).view(torch.int8)
+    want[slots[ok] // bs, slots[ok] % bs] = torch.cat([hi(key), hi(value)], -1)
+    assert torch.equal(kv.transpose(1, 2).cpu(), want)
 
 
 @pytest.mark.parametrize("wg_per_cu", ["1", "2"])
