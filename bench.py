@@ -28,6 +28,7 @@ import time
 REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "int8-kvcache_amd"))
 
+import numpy as np  # noqa: E402
 import torch  # noqa: E402
 
 from kvq import _native, synth  # noqa: E402
@@ -91,24 +92,20 @@ def build_c2(B=128, L=32768, hq=28, hkv=4, d=128, bs=16):
             "hq": hq, "hkv": hkv, "d": d, "bs": bs, "alg_bytes": alg, "kv_bytes": B * L * hkv * d * 2}
 
 
-MIN_LAUNCH_GRID_SIZE_2D = 128   # vLLM's Triton builder: split buffers for up to 128 // kv heads requests
-
-
-def backend_passes_split_buffers(num_reqs, num_tokens, num_kv_heads):
-    """Whether the vLLM backend hands the kernel vLLM's split buffers for this batch (kvq.vllm_int8.backend
-    Int8StaticImpl._split_buffers, reference backend.py:175-177): vLLM's Triton metadata holds them for
-    batches of up to 128 // kv heads requests, with that many rows."""
-    threshold = MIN_LAUNCH_GRID_SIZE_2D // num_kv_heads
-    return num_reqs <= threshold and num_tokens <= threshold
+def backend_passes_split_buffers(q_lens, seq_lens, num_kv_heads):
+    """Whether the vLLM backend hands the kernel its split buffers for this batch, outside graph capture
+    (kvq.vllm_int8.backend Int8StaticBuilder._split_for -> cuda_kernels.split_pays): not for enough
+    short-query requests of even length to fill the GPU in one pass."""
+    return ck.split_pays(np.asarray(q_lens), np.asarray(seq_lens), num_kv_heads, ck.one_pass_fill(DEV))
 
 
 def time_c2(w, steps, warmup, split=True):
     """Step time and attention-kernel time of c2. split: the call carries split buffers allocated once
-    beforehand (as the vLLM backend passes its metadata's softmax_segm_* buffers), sized for the table
-    width by choose_splits; otherwise the one-pass call without them (nothing cut, nothing allocated)."""
+    beforehand, as the vLLM backend's (SPLIT_PIECES pieces per row); otherwise the one-pass call without
+    them (nothing cut, nothing allocated)."""
     out = torch.empty_like(w["q"])
     scale = w["d"] ** -0.5
-    splits = ck.choose_splits(w["bt"].shape[1] * w["bs"]) if split else 1
+    splits = ck.SPLIT_PIECES if split else 1
     segm = ck.split_buffers(w["B"], w["hq"], w["d"], splits, DEV) if split else None
 
     def step():
@@ -382,7 +379,8 @@ def bench_c3(reps=20, one_pass=True):
     cu = torch.arange(65, dtype=torch.int32, device=DEV) * 8
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
-    segm = ck.split_buffers(q.shape[0], hq, d, ck.choose_splits(sets[0][2].shape[1] * bs), DEV)
+    segm = ck.split_buffers(q.shape[0], hq, d, ck.SPLIT_PIECES, DEV)
+    assert backend_passes_split_buffers([8] * 64, lens, hkv)   # the backend's call for this batch
 
     def fn(i, segm=segm):
         kc, vc, bt = sets[i]
@@ -417,7 +415,8 @@ def bench_c4(reps=10, one_pass=True):
     cu = torch.arange(97, dtype=torch.int32, device=DEV)
     sl = torch.tensor(lens, dtype=torch.int32, device=DEV)
     out = torch.empty_like(q)
-    segm = ck.split_buffers(96, hq, d, ck.choose_splits(bt.shape[1] * bs), DEV)
+    segm = ck.split_buffers(96, hq, d, ck.SPLIT_PIECES, DEV)
+    assert backend_passes_split_buffers([1] * 96, lens, hkv)   # the backend's call for this batch
     ms_dec = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st, segm=segm),
                               reps, 1)
     ms_dec1 = _median_event_ms(lambda i: ck.decode_attention(q, kc, vc, out, cu, sl, bt[:96], d ** -0.5, st), reps,
@@ -506,9 +505,14 @@ def main():
     w = build_c2()
     torch.cuda.synchronize()
     print("# timing c2", file=sys.stderr, flush=True)
-    # the call as the vLLM backend makes it for this batch: 128 requests > 128 // 4 kv heads, so no split
-    # buffers (one pass); the call with split buffers is reported beside it
-    split = backend_passes_split_buffers(w["B"], w["B"], w["hkv"])
+    # the call as the vLLM backend makes it for this batch outside graph capture: 128 requests x 4 kv heads
+    # of even length fill the GPU, so no split buffers (one pass); the call with split buffers (what a
+    # captured graph replays) is reported beside it
+    split = backend_passes_split_buffers([1] * w["B"], [w["L"]] * w["B"], w["hkv"])
+    # the other call is timed first, after 30 untimed calls (~20 ms): a GPU that has idled while the host
+    # built the workload runs the first ~20 ms of calls ~3% slower (measured: 668 vs 645 us per kernel,
+    # both variants, whichever runs first), so both timings start from a busy GPU
+    _, ms1, k1_mean, _, s1 = time_c2(w, max(5, args.steps // 2), 30, split=not split)
     out, ms_step, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup, split=split)
     alg = w["alg_bytes"]
     res = {
@@ -525,19 +529,20 @@ def main():
         "config": {"workload": "c2: INT8 paged decode attention, 128 requests x 32768 keys, 28 q / 4 kv heads, "
                                "d128, block 16, vLLM interleaved int8 cache, shuffled block tables",
                    "split_buffers": split, "max_splits": splits,
-                   "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch (no split "
-                           "buffers above 128 // kv heads requests: one pass, nothing allocated)" if not split else
-                           "kvq.cuda_kernels.decode_attention with split buffers",
+                   "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch outside "
+                           "graph capture (enough requests of even length to fill the GPU: no split buffers, one "
+                           "pass, nothing allocated)" if not split else
+                           "kvq.cuda_kernels.decode_attention with split buffers, as the vLLM backend calls it",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / (kern_ms_mean * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(alg / (kern_ms_mean * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
                      "kernel": "attn_kernel<128,3>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
-    _, ms1, k1_mean, _, s1 = time_c2(w, max(5, args.steps // 2), 2, split=not split)
     res["c2_other_call"] = {
-        "what": ("with split buffers allocated once beforehand (%d pieces per row at most): segments cut across "
-                 "workgroups, fp32 partials merged by split_reduce_kernel" % s1) if not split else
+        "what": ("with split buffers allocated once beforehand (%d pieces per row at most, the vLLM backend's "
+                 "buffers, which a captured graph always gets): segments cut across workgroups where the plan "
+                 "calls for it, fp32 partials merged by split_reduce_kernel" % s1) if not split else
                 "without split buffers: one pass, each (request, kv head) whole in one workgroup",
         "us_per_call": round(ms1 * 1e3, 1), "kernel_us_mean": round(k1_mean * 1e3, 1),
         "GBps": round(alg / (ms1 * 1e-3) / 1e9, 1), "frac": round(alg / (ms1 * 1e-3) / 1e9 / PEAK_GBS, 4)}

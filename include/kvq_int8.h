@@ -92,23 +92,29 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
                               float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
                               int64_t target_waves, int64_t max_query_len, int64_t qmax, void* stream);
 
-/* kvq_int8_decode_attention with a choice of q scale granularity: q_group = head_dim is that entry
- * point's one scale per (token, q head); q_group = 32 quantizes q with one scale per 32 channels and
- * sums the groups' scaled integer dots in fp32 -- the reference's numerics configurations
- * B_channel_qgroup32 / B_channel_smooth_qgroup32 (q_gran "group32", kvq/int8_ref.py:120-129), which its
- * CUDA kernel does not implement (kvq/vllm_int8/backend.py:125-128 rejects them); bound by
- * kvq/cuda_kernels.py decode_attention / paged_attention(q_group=32). Other arguments and results as
- * kvq_int8_decode_attention. */
-int kvq_int8_decode_attention_qgroup(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
-                                     int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
-                                     int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
-                                     int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
-                                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
-                                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
-                                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
-                                     double softmax_scale, float* segm_out, float* segm_max, float* segm_sum,
-                                     int64_t seg_st, int64_t seg_sh, int64_t num_splits, int64_t target_waves,
-                                     int64_t max_query_len, int64_t qmax, int64_t q_group, void* stream);
+/* kvq_int8_decode_attention with two additions to the reference's operator, bound by
+ * kvq/cuda_kernels.py decode_attention / paged_attention (q_group=, and split buffers of fewer rows):
+ *  - q_group: head_dim is kvq_int8_decode_attention's one q scale per (token, q head); 32 quantizes q
+ *    with one scale per 32 channels and sums the groups' scaled integer dots in fp32 -- the reference's
+ *    numerics configurations B_channel_qgroup32 / B_channel_smooth_qgroup32 (q_gran "group32",
+ *    kvq/int8_ref.py:120-129), which its CUDA kernel does not implement (kvq/vllm_int8/backend.py:125-128
+ *    rejects them).
+ *  - segm_rows: the split buffers' token rows. The reference indexes them by token and so needs a row
+ *    for every token of q (int8_kv.cu:612-620); here a request whose tokens do not all lie in
+ *    [0, segm_rows) is never cut (it runs whole, written directly), so a caller may pass buffers sized
+ *    for its short requests only -- e.g. for a batch that puts them first -- and still have the longest
+ *    of those cut across workgroups. segm_rows >= T is kvq_int8_decode_attention.
+ * Other arguments and results as kvq_int8_decode_attention. */
+int kvq_int8_decode_attention_ex(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                                 int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                                 int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                 int64_t head_dim, void* out, int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q,
+                                 const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                                 int64_t num_seqs, int64_t num_q_heads, const float* k_scale, int64_t k_scale_cols,
+                                 const float* v_scale, int64_t v_scale_cols, double softmax_scale, float* segm_out,
+                                 float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
+                                 int64_t segm_rows, int64_t target_waves, int64_t max_query_len, int64_t qmax,
+                                 int64_t q_group, void* stream);
 
 /* kvq_int8_decode_attention without split buffers from the caller and without any allocation: no
  * counterpart in the reference. For callers that cannot allocate device memory around the call (code

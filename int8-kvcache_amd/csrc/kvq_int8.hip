@@ -500,6 +500,7 @@ struct AttnArgs {
   int num_blocks, lbs, G, qmax, ks_pc, vs_pc;
   int num_seqs, hkv;
   int max_splits;     // split buffers hold this many pieces per (token, q head); 1 = no split buffers
+  int cut_rows;       // the split buffers' rows: tokens [0, cut_rows); a request with a token beyond is never cut
   int rt;             // row tiles per workgroup: consecutive 16-row tiles of one (request, kv head)
   int ksplit;         // key splits per workgroup: wavefront (t, k) takes every ksplit-th key tile of row tile t
   int waves;          // rt * ksplit wavefronts per workgroup
@@ -532,6 +533,11 @@ __device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
   w.rgroups = (rt + a.rt - 1) / a.rt;
   return w;
 }
+// Whether the request's segments may be cut across workgroups: split buffers exist and hold rows for
+// all of its tokens.
+__device__ __forceinline__ bool cuttable(const AttnArgs& a, const ReqWork& w) {
+  return a.max_splits > 1 && w.tok + w.qlen <= a.cut_rows;
+}
 // Length, in work units, of each of the request's (kv head, row group) segments: seg_cost units for
 // its fixed cost (q load and quantization, the block-table walk's first round trips, the finish and
 // output write -- latency a one-tile segment pays as much as a long one), then one unit per tile.
@@ -545,8 +551,8 @@ __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
 // same amount of work -- K/V to stream plus the segments' fixed costs -- however skewed the request
 // lengths are. chunk is also long enough that no segment is cut into more than max_splits pieces.
 // The merge kernel needs none of it: it reads each segment's piece count from the denominators.
-// Without split buffers (max_splits 1) a workgroup instead runs, whole, every segment that starts
-// inside its range.
+// Segments that may not be cut (no split buffers, or none for the request's tokens) are run whole by the
+// workgroup whose range holds their start.
 struct Plan {
   long long total, chunk;
 };
@@ -564,7 +570,7 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
       const ReqWork w = req_work(a, r);
       const int len = seg_units(a, w);
       v = (long long)len * a.hkv * w.rgroups;
-      nmax = max(nmax, len);
+      if (cuttable(a, w)) nmax = max(nmax, len);
     }
     if (c < PLAN_CACHE) u[c] = v;
     tot += v;
@@ -577,7 +583,7 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
   Plan p;
   p.total = uniform64(tot);
   long long ch = (p.total + a.workers - 1) / a.workers;
-  if (a.max_splits > 1) {
+  if (nmax > 0) {
     ch = max(ch, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
     ch = max(ch, (long long)a.min_tiles);
   }
@@ -1152,7 +1158,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
 #pragma unroll
       for (int i = 0; i < 4; ++i) vsc[t][i] = a.vs_pc ? a.vs[kvh * D + 16 * t + 4 * g + i] : a.vs[kvh];
     if (nparts == 1) {
-      if (a.max_splits > 1 && g == 0)
+      if (a.max_splits > 1 && qt < a.cut_rows && g == 0)
         a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
       const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
       uint16_t* orow = a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + 4 * g;
@@ -1182,7 +1188,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     for (int t = 0; t < VT; ++t) vsc[VT * i + t] = a.vs_pc ? a.vs[kvh * D + OPL * g + VT * i + t] : a.vs[kvh];
   if (nparts == 1) {
     // a row that is not cut tells the merge kernel so: -1 in its piece-0 denominator slot
-    if (a.max_splits > 1 && g == 0)
+    if (a.max_splits > 1 && qt < a.cut_rows && g == 0)
       a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
     const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
     uint32_t o[OPL / 2];
@@ -1247,7 +1253,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   ReqWork w = req_work(a, r);
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
-  const bool whole = a.max_splits == 1;
+  bool whole = !cuttable(a, w);
   int solo = 0;  // pieces run by a single wavefront so far (uniform across the workgroup)
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
@@ -1286,6 +1292,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
         w = req_work(a, r);
       } while (w.ntiles == 0);
       seglen = seg_units(a, w);
+      whole = !cuttable(a, w);
     }
   }
 }
@@ -1710,7 +1717,7 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
     return float4{v, v, v, v};
   };
   if (nparts == 1) {
-    if (a.max_splits > 1 && h == 0) a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
+    if (a.max_splits > 1 && qt < a.cut_rows && h == 0) a.segm_sum[(int64_t)qt * a.seg_st + (int64_t)head * a.seg_sh] = -1.f;
     const float inv = 1.f / __builtin_fmaxf(l, 1e-30f);
     uint16_t* orow = a.out + (int64_t)qt * a.o_st + (int64_t)head * a.o_sh + 4 * h;
 #pragma unroll
@@ -1762,7 +1769,7 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
   ReqWork w = req_work(a, r);
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
-  const bool whole = a.max_splits == 1;
+  bool whole = !cuttable(a, w);
   uint8_t* ring = reinterpret_cast<uint8_t*>(v32_lds);
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
@@ -1787,6 +1794,7 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
         w = req_work(a, r);
       } while (w.ntiles == 0);
       seglen = seg_units(a, w);
+      whole = !cuttable(a, w);
     }
   }
 }
@@ -1858,7 +1866,8 @@ __global__ __launch_bounds__(WAVE * RED_WAVES) void split_reduce_kernel(AttnArgs
   const int h = blockIdx.y * RED_WAVES + __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const int tok = a.cu_q[seq], qlen = a.cu_q[seq + 1] - tok;
   if (h >= a.G * a.hkv || qlen <= 0 || qlen > a.qmax) return;
-  for (int t = blockIdx.z; t < qlen; t += gridDim.z) merge_row<D>(a, tok, t, h, lane);
+  const int rows = min(qlen, a.cut_rows - tok);  // tokens past the split buffers' rows were not cut
+  for (int t = blockIdx.z; t < rows; t += gridDim.z) merge_row<D>(a, tok, t, h, lane);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2631,8 +2640,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
                      int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
                      float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
-                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, int64_t q_group,
-                     void* stream);
+                     int64_t num_splits, int64_t segm_rows, int64_t target_waves, int64_t max_query_len, int64_t qmax,
+                     int64_t q_group, void* stream);
 
 }  // namespace
 
@@ -2765,7 +2774,7 @@ int kvq_stream_scatter(const void* key, int64_t key_st, int64_t key_sh, const vo
   return launched("stream_scatter");
 }
 
-int kvq_abi_version(void) { return 8; }
+int kvq_abi_version(void) { return 9; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 
@@ -2875,27 +2884,29 @@ int kvq_int8_decode_attention(const void* q, int64_t q_st, int64_t q_sh, const i
   return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
                           num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
-                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax, 0, stream);
+                          segm_max, segm_sum, seg_st, seg_sh, num_splits, INT32_MAX, target_waves, max_query_len, qmax, 0,
+                          stream);
 }
 
-int kvq_int8_decode_attention_qgroup(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
-                                     int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
-                                     int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
-                                     int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
-                                     const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
-                                     int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
-                                     int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
-                                     double softmax_scale, float* segm_out, float* segm_max, float* segm_sum,
-                                     int64_t seg_st, int64_t seg_sh, int64_t num_splits, int64_t target_waves,
-                                     int64_t max_query_len, int64_t qmax, int64_t q_group, void* stream) {
+int kvq_int8_decode_attention_ex(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                                 int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                                 int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                                 int64_t head_dim, void* out, int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q,
+                                 const int32_t* seq_lens, const int32_t* block_table, int64_t bt_stride,
+                                 int64_t num_seqs, int64_t num_q_heads, const float* k_scale, int64_t k_scale_cols,
+                                 const float* v_scale, int64_t v_scale_cols, double softmax_scale, float* segm_out,
+                                 float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh, int64_t num_splits,
+                                 int64_t segm_rows, int64_t target_waves, int64_t max_query_len, int64_t qmax,
+                                 int64_t q_group, void* stream) {
   if (q_group != 32 && q_group != head_dim)
-    return fail("int8_decode_attention_qgroup: q_group must be 32 or head_dim (%lld), got %lld", (long long)head_dim,
+    return fail("int8_decode_attention_ex: q_group must be 32 or head_dim (%lld), got %lld", (long long)head_dim,
                 (long long)q_group);
+  if (segm_rows < 0) return fail("int8_decode_attention_ex: segm_rows must be >= 0");
   return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
                           num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, segm_out,
-                          segm_max, segm_sum, seg_st, seg_sh, num_splits, target_waves, max_query_len, qmax,
-                          q_group == 32 ? 32 : 0, stream);
+                          segm_max, segm_sum, seg_st, seg_sh, num_splits, segm_rows, target_waves, max_query_len,
+                          qmax, q_group == 32 ? 32 : 0, stream);
 }
 
 int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh, int64_t num_tokens,
@@ -2934,7 +2945,7 @@ int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh,
   return decode_attention(q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn, v_sh, num_blocks, block_size,
                           num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q, seq_lens, block_table, bt_stride,
                           num_seqs, num_q_heads, k_scale, k_scale_cols, v_scale, v_scale_cols, softmax_scale, so, sm,
-                          ss, st_t, st_h, num_splits, target_waves, max_query_len, qmax, 0, stream);
+                          ss, st_t, st_h, num_splits, num_tokens, target_waves, max_query_len, qmax, 0, stream);
 }
 
 int kvq_noalloc_scratch_bytes(void) { return (int)NOALLOC_SCRATCH_BYTES; }
@@ -2950,8 +2961,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
                      int64_t bt_stride, int64_t num_seqs, int64_t num_q_heads, const float* k_scale,
                      int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols, double softmax_scale,
                      float* segm_out, float* segm_max, float* segm_sum, int64_t seg_st, int64_t seg_sh,
-                     int64_t num_splits, int64_t target_waves, int64_t max_query_len, int64_t qmax, int64_t q_group,
-                     void* stream) {
+                     int64_t num_splits, int64_t segm_rows, int64_t target_waves, int64_t max_query_len, int64_t qmax,
+                     int64_t q_group, void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("int8_decode_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("int8_decode_attention: block_size must be a power of two >= 16");
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads)
@@ -2961,7 +2972,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   if (num_seqs == 0) { g_err.clear(); return KVQ_OK; }
   if ((k_scale_cols != 1 && k_scale_cols != head_dim) || (v_scale_cols != 1 && v_scale_cols != head_dim))
     return fail("int8_decode_attention: scale columns must be 1 or head_dim");
-  if (num_splits > 1 && (!segm_out || !segm_max || !segm_sum)) return fail("int8_decode_attention: split buffers missing");
+  if (num_splits > 1 && segm_rows > 0 && (!segm_out || !segm_max || !segm_sum))
+    return fail("int8_decode_attention: split buffers missing");
   if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_st | q_sh | o_st | o_sh) % 8 ||
       (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 16 || (segm_out && !aligned16(segm_out)))
     return fail("int8_decode_attention: rows must be 16-byte aligned (base pointers and strides)");
@@ -3000,7 +3012,9 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.qmax = (int)std::min<int64_t>(qmax, INT32_MAX);
   a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
-  a.max_splits = (int)num_splits; a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? 1 : ks; a.waves = waves;
+  a.max_splits = (int)num_splits;
+  a.cut_rows = num_splits > 1 ? (int)std::min<int64_t>(segm_rows, INT32_MAX) : 0;
+  a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? 1 : ks; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES * a.ksplit;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
@@ -3041,7 +3055,7 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   hipLaunchKernelGGL(kern, grid, block, lds, st, a);
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);
-  if (rc != KVQ_OK || num_splits == 1) return rc;
+  if (rc != KVQ_OK || num_splits == 1 || a.cut_rows == 0) return rc;
   const dim3 rgrid((unsigned)num_seqs, (unsigned)((num_q_heads + RED_WAVES - 1) / RED_WAVES), (unsigned)maxq);
   if (head_dim == 128) hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
   else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);

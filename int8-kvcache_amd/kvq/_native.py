@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -22,10 +22,10 @@ SIGNATURES = {
     "kvq_int8_decode_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                   _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr, _i64,
                                   _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64, _ptr],
-    "kvq_int8_decode_attention_qgroup": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
-                                         _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr,
-                                         _i64, _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64,
-                                         _i64, _ptr],
+    "kvq_int8_decode_attention_ex": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64,
+                                     _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _ptr,
+                                     _i64, _ptr, _i64, _f64, _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _i64, _i64, _ptr],
     "kvq_int8_decode_attention_noalloc": [_ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64,
                                           _i64, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64,
                                           _i64, _ptr, _i64, _ptr, _i64, _f64, _i64, _i64, _i64, _i64, _ptr],

@@ -142,8 +142,8 @@ class _Ext:
         if split:
             _check(segm_out is not None and segm_sum is not None, "int8_decode_attention: split buffers missing")
             for t in (segm_out, segm_max, segm_sum):
-                _check(t.dtype == torch.float32 and t.shape[0] >= q.shape[0] and t.shape[1] == Hq and t.shape[2] == S,
-                       "int8_decode_attention: split buffers must be float32 [>= T, Hq, S(, D)]")
+                _check(t.dtype == torch.float32 and t.shape[0] == segm_max.shape[0] and t.shape[1] == Hq and
+                       t.shape[2] == S, "int8_decode_attention: split buffers must be float32 [rows, Hq, S(, D)]")
             _check(segm_max.stride(2) == 1 and segm_sum.stride() == segm_max.stride(),
                    "int8_decode_attention: segm_max / segm_sum layouts differ")
             seg_st, seg_sh = segm_max.stride(0), segm_max.stride(1)
@@ -159,8 +159,11 @@ class _Ext:
                 segm_out.data_ptr() if split else None, segm_max.data_ptr() if split else None,
                 segm_sum.data_ptr() if split else None, seg_st, seg_sh, S, _target_waves(), int(max_query_len),
                 int(qmax)]
-        if grouped:
-            _native.call("kvq_int8_decode_attention_qgroup", *args, 32, _stream(q))
+        rows = segm_max.shape[0] if split else 0
+        if grouped or rows < q.shape[0]:
+            # tokens past the buffers' rows are never cut (kvq_int8_decode_attention_ex)
+            args.insert(-3, rows)
+            _native.call("kvq_int8_decode_attention_ex", *args, 32 if grouped else d, _stream(q))
         else:
             _native.call("kvq_int8_decode_attention", *args, _stream(q))
 
@@ -259,6 +262,33 @@ def split_buffers(num_tokens, num_q_heads, head_dim, splits, device):
             torch.empty(num_tokens, num_q_heads, splits, dtype=torch.float32, device=device))
 
 
+SPLIT_PIECES = 16        # pieces per (request, kv head) of the vLLM backend's split buffers (as vLLM's own)
+EVEN_LENGTHS = 1.05      # a batch whose longest short request is within this factor of the mean is even
+
+
+def one_pass_fill(device):
+    """(request, kv head) pairs that fill the device in one pass: two workgroups per CU."""
+    dev = torch.device(device)
+    return 2 * (torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 256)
+
+
+def split_pays(query_lens, seq_lens, num_kv_heads, fill):
+    """Whether split buffers pay for a batch, from host-side lengths (numpy; seq_lens None = unknown): with
+    them the kernel cuts the longest (request, kv head) pairs across workgroups and merges the pieces in
+    a second launch; without, each pair runs whole in one workgroup. One pass serves as well only when
+    the short-query requests (1..SHORT_Q tokens) give at least `fill` pairs and their lengths are within
+    EVEN_LENGTHS of even. False when no request has a short query."""
+    q = np.asarray(query_lens)
+    short = (q >= 1) & (q <= SHORT_Q)
+    n = int(short.sum())
+    if n == 0:
+        return False
+    if seq_lens is None or n * num_kv_heads < fill:
+        return True
+    ls = np.asarray(seq_lens)[:len(q)][short].astype(np.int64)
+    return int(ls.max()) * n > EVEN_LENGTHS * int(ls.sum())
+
+
 def _target_waves():
     """Wavefronts the kernel spreads a batch over (KVQ_TARGET_WAVES; 0 = as many as the kernel keeps resident)."""
     return int(os.environ.get("KVQ_TARGET_WAVES", "0"))
@@ -269,10 +299,13 @@ def decode_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_tab
     """INT8 attention for the requests with at most SHORT_Q query tokens (others are skipped).
     max_query_len bounds the short queries' length (reference kvq/cuda_kernels.py:51-58).
 
-    segm = (segm_out [T, Hq, S, D], segm_max [T, Hq, S], segm_sum [T, Hq, S]) allows up to S pieces per
+    segm = (segm_out [R, Hq, S, D], segm_max [R, Hq, S], segm_sum [R, Hq, S]) allows up to S pieces per
     (request, kv head) (the reference always uses S); the kernel gives each as many of them as its share
-    of the batch's work calls for. Without segm nothing is cut and nothing is allocated: one pass, each
-    (request, kv head) whole in one workgroup (the reference's S = 1, kvq/cuda/int8_kv.cu:612-613).
+    of the batch's work calls for. The reference needs R >= T (its buffers are indexed by token); here a
+    request with a token at or past row R is simply never cut, so buffers sized for the short requests
+    of a batch that puts them first serve it too. Without segm nothing is cut and nothing is allocated:
+    one pass, each (request, kv head) whole in one workgroup (the reference's S = 1,
+    kvq/cuda/int8_kv.cu:612-613).
 
     q_group: None (one q scale per (token, q head), the reference kernel's numerics) or 32 (one per 32
     channels: the B_*_qgroup32 configurations of kvq/int8_ref.py:120-129, an addition to the reference's

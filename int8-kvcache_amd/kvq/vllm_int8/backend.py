@@ -12,6 +12,9 @@ kvq.vllm_plugin registers the class), and
                     B_channel_smooth_qgroup32, B_channel_qgroup32 (q scales per 32 channels)
   KVQ_KERNEL        "cuda" (default; the name is kept for compatibility -- it selects these HIP kernels)
 
+  KVQ_SPLIT_MB      device memory of the backend's split buffers (default 256; 0: none, every request
+                    whole in one workgroup)
+
 Per step and layer the backend
   * writes the step's new K/V into the int8 cache quantized with the static scales
     (do_kv_cache_update -> quant_reshape_and_cache); vLLM's cache is [num_blocks, H, block_size, 2 D],
@@ -19,12 +22,19 @@ Per step and layer the backend
   * runs attention (forward -> paged_attention): requests with more than cuda_kernels.SHORT_Q query
     tokens through dequant_pages + the bf16 prefill kernel (their page plan is made once per step in the
     metadata builder), the others through the INT8 MFMA kernel, with q quantized on the fly.
+The INT8 kernel balances a batch by cutting its longest (request, kv head) pairs across workgroups; the
+cut pieces go to split buffers that the builder allocates once, sized for the short-query tokens of a
+full batch (vLLM's own split buffers hold only 128 // kv-heads requests' rows, and the reference passes
+them only to batches that small). Short-query requests are ordered first (reorder_batch_threshold), so
+their tokens are the buffers' rows. Each step the builder passes them unless the batch is one that a
+single pass serves as well: enough requests to fill the GPU and lengths within 5% of even.
 Full graphs are offered only for uniform batches the INT8 kernel covers alone (the long-query path sizes
 buffers from host-side lengths).
 """
 import os
 from typing import ClassVar
 
+import numpy as np
 import torch
 from vllm.logger import init_logger
 from vllm.v1.attention.backend import AttentionCGSupport
@@ -51,6 +61,7 @@ KERNEL_CONFIGS = {
     "B_channel_smooth_qgroup32": ("per_channel", True, 32),
     "B_channel_qgroup32": ("per_channel", False, 32),
 }
+SPLIT_PIECES = cuda_kernels.SPLIT_PIECES   # pieces per (request, kv head) the split buffers hold
 DRAFT_PREFIX_END = "model.layers"   # a draft layer "draft_model.model.layers.<i>..." is "model.layers.<i>..."
                                     # in the draft's own calibration file
 
@@ -118,14 +129,17 @@ class Int8StaticBackend(TritonAttentionBackend):
 
 
 class Int8StaticBuilder(TritonAttentionMetadataBuilder):
-    """Triton-backend metadata (lengths, block table, split-KV buffers) plus, when a step holds
-    long-query requests, their temporary bf16 page plan (cuda_kernels.plan_long, built once per step for
+    """Triton-backend metadata (lengths, block table) plus the split buffers this step's INT8 call gets
+    (kvq_segm, see _split_for) and, when a step holds long-query requests, their temporary bf16 page plan (cuda_kernels.plan_long, built once per step for
     all layers). vLLM creates the builder after loading the model and before capturing graphs, so it is
     where every layer receives its static scales: persistent GPU tensors captured graphs keep pointing
     at (reference backend.py:68-115)."""
 
     # a draft-decode step that reuses an older metadata object would also reuse its long-query plan
     supports_draft_decode_metadata_update = False
+    # requests with at most SHORT_Q query tokens first: their tokens are then rows [0, n) of the batch,
+    # the rows the split buffers hold
+    reorder_batch_threshold = cuda_kernels.SHORT_Q
 
     @classmethod
     def get_cudagraph_support(cls, vllm_config, kv_cache_spec):
@@ -148,8 +162,43 @@ class Int8StaticBuilder(TritonAttentionMetadataBuilder):
         for layer in layer_names:
             src, key = _layer_scale_set(layer, path)
             layers[layer].impl.set_static(scales.for_layer(src, key, *tp, device))
-        logger.info("kvq: static INT8 scales for %d layers from %s (tp %d/%d, cfg %s, MI355X kernels)",
-                    len(layer_names), path, tp[0], tp[1], os.environ.get("KVQ_CFG", DEFAULT_CFG))
+        impl = layers[layer_names[0]].impl if layer_names else None
+        self.kvq_hkv = impl.num_kv_heads if impl else 1
+        self.kvq_segm = self._split_buffers_for(vllm_config, impl.num_heads, impl.head_size, device) if impl else None
+        self.kvq_fill = cuda_kernels.one_pass_fill(device)
+        logger.info("kvq: static INT8 scales for %d layers from %s (tp %d/%d, cfg %s, MI355X kernels, split "
+                    "buffers for %d tokens)", len(layer_names), path, tp[0], tp[1],
+                    os.environ.get("KVQ_CFG", DEFAULT_CFG), 0 if self.kvq_segm is None else self.kvq_segm[1].shape[0])
+
+    @staticmethod
+    def _split_buffers_for(vllm_config, num_heads, head_size, device):
+        """Split buffers [rows, Hq, SPLIT_PIECES(, D)] for the short-query tokens of a full batch
+        (max_num_seqs requests of 1 + speculative tokens each), within KVQ_SPLIT_MB; None if none fit.
+        Allocated once, before graph capture; every layer's call reuses them (calls are stream-ordered)."""
+        spec = vllm_config.speculative_config
+        per_req = min(cuda_kernels.SHORT_Q, 1 if spec is None else 1 + spec.num_speculative_tokens)
+        per_row = num_heads * SPLIT_PIECES * (head_size + 2) * 4
+        budget = int(float(os.environ.get("KVQ_SPLIT_MB", "256")) * 2 ** 20)
+        rows = min(vllm_config.scheduler_config.max_num_seqs * per_req, budget // per_row)
+        if rows <= 0:
+            return None
+        return cuda_kernels.split_buffers(rows, num_heads, head_size, SPLIT_PIECES, device)
+
+    def _split_for(self, c, capturing=False):
+        """The split buffers for this step, or None where one pass serves as well (cuda_kernels.split_pays:
+        enough short-query requests to fill the GPU, host-side lengths even). A graph being captured always
+        gets them: its replays see other lengths, and the kernel cuts only what the lengths it reads on
+        the device call for."""
+        if self.kvq_segm is None:
+            return None
+        if capturing:
+            return self.kvq_segm
+        lens = getattr(c, "seq_lens_cpu_upper_bound", None)
+        if lens is None:
+            lens = getattr(c, "seq_lens_cpu", None)
+        pays = cuda_kernels.split_pays(np.diff(c.query_start_loc_cpu.numpy()), None if lens is None else lens.numpy(),
+                                       self.kvq_hkv, self.kvq_fill)
+        return self.kvq_segm if pays else None
 
     def build(self, common_prefix_len, common_attn_metadata, fast_build=False):
         md = super().build(common_prefix_len, common_attn_metadata, fast_build)
@@ -160,6 +209,12 @@ class Int8StaticBuilder(TritonAttentionMetadataBuilder):
             upper = getattr(c, "seq_lens_cpu_upper_bound", None)
             md.kvq_long = cuda_kernels.plan_long(c.query_start_loc_cpu, c.seq_lens.cpu() if upper is None else upper,
                                                  self.block_size)
+        md.kvq_segm = self._split_for(c)
+        return md
+
+    def build_for_cudagraph_capture(self, common_attn_metadata):
+        md = super().build_for_cudagraph_capture(common_attn_metadata)
+        md.kvq_segm = self._split_for(common_attn_metadata, capturing=True)
         return md
 
 
@@ -203,15 +258,6 @@ class Int8StaticImpl(TritonAttentionImpl):
         k_cache, v_cache = self._caches(kv_cache)
         cuda_kernels.quant_reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, self.static)
 
-    @staticmethod
-    def _split_buffers(md, num_tokens, num_reqs):
-        """vLLM's split-KV buffers when this batch fits them (the Triton backend's own rule: at most
-        seq_threshold_3D requests, no more tokens than the buffers' rows); otherwise None, and the INT8
-        kernel runs in one pass."""
-        if num_reqs > md.seq_threshold_3D or num_tokens > md.softmax_segm_max.shape[0]:
-            return None
-        return md.softmax_segm_output, md.softmax_segm_max, md.softmax_segm_expsum
-
     def forward(self, layer, query, key, value, kv_cache, attn_metadata, output, output_scale=None,
                 output_block_scale=None):
         if attn_metadata is None:
@@ -219,8 +265,8 @@ class Int8StaticImpl(TritonAttentionImpl):
         md = attn_metadata
         n = md.num_actual_tokens
         k_cache, v_cache = self._caches(kv_cache)
-        segm = self._split_buffers(md, n, md.query_start_loc.shape[0] - 1)
         cuda_kernels.paged_attention(query[:n], k_cache, v_cache, output[:n], md.query_start_loc, md.seq_lens,
                                      md.block_table, md.max_query_len, self.scale, self.static,
-                                     getattr(md, "kvq_long", None), segm, q_group=self.q_group)
+                                     getattr(md, "kvq_long", None), getattr(md, "kvq_segm", None),
+                                     q_group=self.q_group)
         return output

@@ -341,6 +341,43 @@ def test_no_split_buffers_means_one_pass_and_no_allocation():
     assert torch.equal(outs[0], outs[1])
 
 
+SPLIT_ROW_BATCHES = {
+    # verification rows (56 per kv head: the 32-row kernel) around a long request
+    "verify": ([1, 4, 40, 8, 1, 3, 1, 1], [6000, 3000, 500, 9000, 2100, 7000, 33, 12000], 8),
+    # decode rows (the 16-row kernel with key splits) around a long request
+    "decode": ([1, 1, 1, 40, 1, 1, 1, 1, 1, 1], [6000, 3000, 9000, 500, 2100, 7000, 33, 12000, 1, 4000], 1),
+}
+
+
+@pytest.mark.parametrize("batch", list(SPLIT_ROW_BATCHES))
+@pytest.mark.parametrize("rows", [0, 1, 5, 13, 22])
+def test_split_buffers_with_fewer_rows_than_tokens(batch, rows):
+    """Split buffers of R < T token rows (kvq_int8_decode_attention_ex): requests whose tokens all lie
+    below R may be cut, the others run whole; every short row matches the oracle, long requests are left
+    alone, and nothing is written past the buffers' R rows."""
+    q_lens, seq_lens, maxq = SPLIT_ROW_BATCHES[batch]
+    c = synth.paged_case(28, 4, q_lens, seq_lens, seed=41, params=synth.channel_params(4, 128))
+    c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    T = d["q"].shape[0]
+    assert rows < T
+    full = nan_segm(rows + 2, 28, 8, 128)
+    segm = tuple(t[:rows] for t in full)
+    out = torch.full_like(d["q"], 7.0)
+    ck.decode_attention(d["q"], dev(kq), dev(vq), out, d["cu"], d["seq_lens"], d["block_table"], c["scale"],
+                        d["static"], segm=segm, max_query_len=maxq)
+    torch.cuda.synchronize()
+    for t in full:
+        assert torch.isnan(t[rows:]).all()
+    short = short_rows(c["cu"])
+    o = out.cpu()
+    assert (o[~short] == 7.0).all()
+    ref = oracle_attention(c, kq, vq)
+    check_attention(ref[short], o[short], "split_rows_below_tokens", batch=batch, rows=rows)
+
+
 @pytest.mark.parametrize("reported", [1, 3])
 def test_split_merge_covers_underreported_max_query_len(reported):
     """A caller that reports a smaller max_query_len than the batch holds still gets every row of every

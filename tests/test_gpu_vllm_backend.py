@@ -2,8 +2,9 @@
 149-184): the step's K/V are written into vLLM's interleaved int8 cache by do_kv_cache_update (codes
 bit-exact against the oracle), and forward() answers a mixed batch -- decode rows, speculative
 verification rows, long prefill rows -- through the metadata builder's plan and split buffers, within
-the attention bars against the oracle -- with vLLM's split buffers (few requests) and without them (more
-requests or tokens than the buffers hold: one pass). vLLM itself is replaced by tests/vllm_stub."""
+the attention bars against the oracle -- with the builder's split buffers (few requests, skewed lengths,
+more short tokens than the buffers' rows) and without them (many requests of even length: one pass).
+vLLM itself is replaced by tests/vllm_stub."""
 import os
 import sys
 from types import SimpleNamespace
@@ -27,12 +28,16 @@ HQ, HKV, D, BS = 28, 4, 128, 16
 
 
 BATCHES = {
-    # decode, verification and long prefill rows: more tokens than the split buffers' rows -> one pass
-    "mixed": ([1, 4, 1, 40, 1, 8, 130, 1], [700, 64, 1, 40, 2049, 300, 500, 33], False),
-    # few short requests: vLLM's split buffers are passed (the split path)
+    # decode, verification and long prefill rows, short ones after the long (tokens past the buffers'
+    # 64 rows: run whole)
+    "mixed": ([1, 4, 1, 40, 1, 8, 130, 1], [700, 64, 1, 40, 2049, 300, 500, 33], True),
+    # few short requests
     "short_split": ([1, 4, 1, 8, 1, 3, 1, 1], [700, 64, 1, 2300, 2049, 300, 5000, 33], True),
-    # more requests than seq_threshold_3D (128 // 4 kv heads = 32): no buffers -> one pass
-    "many_decode": ([1] * 38 + [5, 20], [int(x) for x in synth.rng(5).integers(1, 4000, 38)] + [900, 700], False),
+    # skewed decode batch with more short tokens than the buffers' 64 rows
+    "many_decode": ([1] * 90 + [5, 20, 3], [int(x) for x in synth.rng(5).integers(1, 4000, 90)] + [9000, 700, 300],
+                    True),
+    # enough requests to fill the GPU (x 4 kv heads >= 2 per CU), even lengths: one pass
+    "many_even": ([1] * 140, [1500] * 140, False),
 }
 
 
@@ -59,6 +64,7 @@ def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg, batch):
                            speculative_config=None,
                            model_config=SimpleNamespace(num_heads=HQ, num_kv_heads=HKV, head_size=D),
                            scheduler_config=SimpleNamespace(max_num_seqs=64))
+    monkeypatch.setenv("KVQ_SPLIT_MB", "256")
     builder = backend.Int8StaticBuilder(SimpleNamespace(block_size=BS), [name], vcfg, DEV)
 
     # write every request's K/V through the backend, in two steps (history, then the step's tokens)
@@ -86,12 +92,14 @@ def test_backend_step_matches_oracle(tmp_path, monkeypatch, cfg, batch):
     common = CommonAttentionMetadata(query_start_loc=cu.to(DEV), query_start_loc_cpu=cu,
                                      seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=DEV), num_reqs=B,
                                      num_actual_tokens=int(cu[-1]), max_query_len=max(q_lens), max_seq_len=max(seq_lens),
-                                     block_table_tensor=bt.to(DEV), slot_mapping=slots.to(DEV))
+                                     block_table_tensor=bt.to(DEV), slot_mapping=slots.to(DEV),
+                                     seq_lens_cpu_upper_bound=torch.tensor(seq_lens, dtype=torch.int32))
     md = builder.build(0, common)
     has_long = max(q_lens) > 8
     assert (md.kvq_long is not None) == has_long and (not has_long or md.kvq_long.has_short)
     T = int(cu[-1])
-    assert (impl._split_buffers(md, T, B) is not None) == with_buffers
+    assert (md.kvq_segm is not None) == with_buffers
+    assert builder.kvq_segm[1].shape[0] == 64
     q = c["q"].to(DEV)
     out = nan_like(torch.empty(T + 3, HQ, D, dtype=torch.bfloat16, device=DEV))   # vLLM pads the output
     impl.forward(None, q, None, None, kv_cache, md, out)

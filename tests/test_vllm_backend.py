@@ -127,22 +127,6 @@ def test_cache_views_split_the_interleaved_layout(monkeypatch):
     assert kc[2, 5, 1, 7] == kv[2, 1, 5, 7] and vc[2, 5, 1, 7] == kv[2, 1, 5, D + 7]
 
 
-def test_split_buffers_follow_the_triton_builders_rule(monkeypatch):
-    """forward passes vLLM's split buffers only to batches that fit them: at most seq_threshold_3D
-    requests (128 // kv heads) and no more tokens than the buffers' rows; otherwise the INT8 kernel
-    runs in one pass (reference backend.py:175-177)."""
-    from vllm.v1.attention.backends.triton_attn import TritonAttentionMetadataBuilder
-    b = TritonAttentionMetadataBuilder(SimpleNamespace(block_size=BS), [], _vllm_config({}), "cpu")
-    assert b.seq_threshold_3D == 128 // HKV == b.softmax_segm_max.shape[0]
-    md = b.build(0, _common([1] * 4, [10] * 4))
-    impl = _impl(monkeypatch=monkeypatch)
-    bufs = impl._split_buffers(md, 4, 4)
-    assert bufs[0] is b.softmax_segm_output and bufs[1] is b.softmax_segm_max and bufs[2] is b.softmax_segm_expsum
-    assert impl._split_buffers(md, 32, 32) is not None
-    assert impl._split_buffers(md, 33, 33) is None          # more requests than the threshold
-    assert impl._split_buffers(md, 40, 3) is None           # more tokens than the buffers' rows
-
-
 def test_forward_profiling_run_zeroes_output(monkeypatch):
     impl = _impl(monkeypatch=monkeypatch)
     out = torch.ones(4, HQ, D)
@@ -216,6 +200,55 @@ def test_builder_plans_the_long_queries_once_per_step(tmp_path, monkeypatch):
     for f in ("src_req", "src_j", "block_table"):
         assert np.array_equal(getattr(md.kvq_long, f), getattr(ref, f))
     assert md.kvq_long.max_seqlen_k == 910
+
+
+def _split_builder(tmp_path, monkeypatch, spec_tokens=None, max_num_seqs=32):
+    _write_scales(tmp_path / "s.safetensors", ["l0"])
+    monkeypatch.setenv("KVQ_SCALES", str(tmp_path / "s.safetensors"))
+    return backend.Int8StaticBuilder(SimpleNamespace(block_size=BS), ["l0"],
+                                     _vllm_config({"l0": _impl(monkeypatch=monkeypatch)}, spec_tokens, max_num_seqs),
+                                     "cpu")
+
+
+@pytest.mark.parametrize("spec,max_seqs,mb,rows", [(None, 32, None, 32), (3, 32, None, 128), (9, 32, None, 256),
+                                                   (None, 4096, None, 256 * 2 ** 20 // (HQ * 16 * (D + 2) * 4)),
+                                                   (None, 32, "0", 0)])
+def test_builder_split_buffers_cover_a_full_batchs_short_tokens(tmp_path, monkeypatch, spec, max_seqs, mb, rows):
+    """The builder's own split buffers: max_num_seqs x (1 + speculative tokens, at most SHORT_Q) token rows
+    of HQ x 16 pieces, within KVQ_SPLIT_MB (default 256 MiB); none at KVQ_SPLIT_MB=0."""
+    if mb is not None:
+        monkeypatch.setenv("KVQ_SPLIT_MB", mb)
+    b = _split_builder(tmp_path, monkeypatch, spec, max_seqs)
+    if rows == 0:
+        assert b.kvq_segm is None
+        return
+    so, sm, ss = b.kvq_segm
+    assert tuple(so.shape) == (rows, HQ, backend.SPLIT_PIECES, D) and tuple(sm.shape) == tuple(ss.shape) == (rows, HQ, 16)
+    assert so.dtype == sm.dtype == ss.dtype == torch.float32
+
+
+def test_builder_passes_split_buffers_unless_one_pass_serves(tmp_path, monkeypatch):
+    """Per step: split buffers for batches with too few (request, kv head) pairs to fill the GPU, for
+    skewed lengths and when host lengths are unknown; none for many requests of even length, or when no
+    request has a short query. A graph being captured always gets them."""
+    b = _split_builder(tmp_path, monkeypatch, max_num_seqs=256)
+    assert b.kvq_fill == 512 and backend.Int8StaticBuilder.reorder_batch_threshold == ck.SHORT_Q
+    n = b.kvq_fill // HKV                                     # requests that fill the GPU
+    even = torch.full((n,), 4096, dtype=torch.int32)
+    assert b.build(0, _common([1] * (n - 1), [4096] * (n - 1), upper=even[:n - 1])).kvq_segm is b.kvq_segm
+    assert b.build(0, _common([1] * n, [4096] * n, upper=even)).kvq_segm is None
+    nearly = even.clone()
+    nearly[0] = 4300                                          # max / mean just under 1.05: still even
+    assert b.build(0, _common([1] * n, nearly.tolist(), upper=nearly)).kvq_segm is None
+    skew = even.clone()
+    skew[0] = 32768
+    assert b.build(0, _common([1] * n, skew.tolist(), upper=skew)).kvq_segm is b.kvq_segm
+    assert b.build(0, _common([1] * n, [4096] * n)).kvq_segm is b.kvq_segm            # no host lengths
+    # long-query requests do not count: the short ones alone are too few
+    mixed = _common([1] * (n - 1) + [100], [4096] * n, upper=torch.full((n,), 4096, dtype=torch.int32))
+    assert b.build(0, mixed).kvq_segm is b.kvq_segm
+    assert b.build(0, _common([100, 40], [900, 500], upper=torch.tensor([900, 500]))).kvq_segm is None
+    assert b.build_for_cudagraph_capture(_common([1] * n, [4096] * n, upper=even)).kvq_segm is b.kvq_segm
 
 
 @pytest.mark.parametrize("spec,level", [(None, "UNIFORM_BATCH"), (7, "UNIFORM_BATCH"), (8, "UNIFORM_SINGLE_TOKEN_DECODE")])

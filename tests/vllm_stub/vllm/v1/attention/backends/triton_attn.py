@@ -1,6 +1,7 @@
 """The Triton attention backend's classes as the kvq backend uses them: constructor arguments,
 attributes, and the metadata fields read in forward (query_start_loc, seq_lens, block_table,
-max_query_len, num_actual_tokens, seq_threshold_3D and the split-KV buffers softmax_segm_*)."""
+max_query_len, num_actual_tokens, seq_threshold_3D and the split-KV buffers softmax_segm_*), and the
+builder's hooks the kvq builder overrides (build, build_for_cudagraph_capture)."""
 from dataclasses import dataclass
 
 import torch
@@ -83,6 +84,10 @@ class TritonAttentionMetadataBuilder:
             slot_mapping=c.slot_mapping, seq_threshold_3D=self.seq_threshold_3D,
             softmax_segm_output=self.softmax_segm_output, softmax_segm_max=self.softmax_segm_max,
             softmax_segm_expsum=self.softmax_segm_expsum)
+
+    def build_for_cudagraph_capture(self, common_attn_metadata):
+        """vLLM's AttentionMetadataBuilder default: the metadata a graph is captured with."""
+        return self.build(0, common_attn_metadata)
 
 
 class TritonAttentionImpl:
