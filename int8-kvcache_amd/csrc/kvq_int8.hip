@@ -521,14 +521,15 @@ __device__ __forceinline__ long long uniform64(long long x) {
 // What one request asks of the kernel: its 32-key tiles (at least one) and row groups (of `waves`
 // 16-row tiles of (token, q head) rows per kv head). Requests with q_len outside [1, qmax] ask nothing.
 struct ReqWork {
-  int ntiles, rgroups, tok, qlen;
+  int ntiles, rgroups, tok, qlen, len;   // len: the request's key count (seq_lens)
 };
 __device__ __forceinline__ ReqWork req_work(const AttnArgs& a, int r) {
-  ReqWork w{0, 0, 0, 0};
+  ReqWork w{0, 0, 0, 0, 0};
   w.tok = a.cu_q[r];
   w.qlen = a.cu_q[r + 1] - w.tok;
+  w.len = a.seq_lens[r];
   if (w.qlen <= 0 || w.qlen > a.qmax) return w;
-  w.ntiles = max(1, (a.seq_lens[r] + TILE - 1) / TILE);
+  w.ntiles = max(1, (w.len + TILE - 1) / TILE);
   const int rt = (w.qlen * a.G + 15) / 16;
   w.rgroups = (rt + a.rt - 1) / a.rt;
   return w;
@@ -556,32 +557,78 @@ __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
 struct Plan {
   long long total, chunk;
 };
-// The plan (total units, chunk) and the search for the request holding unit `pos0` = worker * chunk,
-// in one pass over the requests (their work is read once; up to PLAN_CACHE * 64 requests stay in registers).
+
+// Inclusive prefix sum / maximum of x over the wavefront's 64 lanes on DPP: row shifts by 1, 2, 4, 8
+// within each 16-lane row, then lane 15's value added into rows 1 and 3 and lane 31's into rows 2
+// and 3 -- VALU instructions only, no LDS round trips. max takes x >= 0.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return x;
+}
+__device__ __forceinline__ int wave_incl_max(int x) {
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, true));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+  x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
+  return x;
+}
+// Inclusive prefix sum of the lanes' v (>= 0): in 32 bits on DPP when every v < 2^24 (64 of them cannot
+// overflow), otherwise by 64-bit shuffles.
+constexpr long long PLAN_FAST_MAX = 1ll << 24;
+__device__ __forceinline__ long long wave_incl_sum64(long long v, int lane) {
+  if (__ballot(v >= PLAN_FAST_MAX) == 0ull) return (long long)wave_incl_sum((int)v);
+  long long incl = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const long long y = __shfl_up(incl, o, WAVE);
+    if (lane >= o) incl += y;
+  }
+  return incl;
+}
+__device__ __forceinline__ long long lane_value64(long long x, int l) {
+  const unsigned lo = __builtin_amdgcn_readlane((unsigned)(x & 0xffffffffll), l);
+  const unsigned hi = __builtin_amdgcn_readlane((unsigned)((unsigned long long)x >> 32), l);
+  return (long long)(((unsigned long long)hi << 32) | lo);
+}
+
+// The plan (total units, chunk) and the request holding unit pos0 = worker * chunk -- its index, the
+// unit its segments start at and its work -- in two scans over the requests (their work is read once;
+// up to PLAN_CACHE * 64 requests stay in registers). Every workgroup computes the same plan at once
+// from the same few lines of cu_seqlens_q / seq_lens, so the scans run on DPP rather than through LDS
+// permutes (the plan took ~7 us of a 62 us verification batch with 64-bit shuffle reductions).
 constexpr int PLAN_CACHE = 4;
-__device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_out, long long& start_out) {
+__device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_out, long long& start_out,
+                                ReqWork& w_out) {
   long long u[PLAN_CACHE];
+  int tk[PLAN_CACHE], ql[PLAN_CACHE], ln[PLAN_CACHE];
   long long tot = 0;
   int nmax = 0;
   for (int c = 0; c * WAVE < a.num_seqs; ++c) {
     const int r = c * WAVE + lane;
     long long v = 0;
+    int len = 0;
+    ReqWork w{0, 0, 0, 0, 0};
     if (r < a.num_seqs) {
-      const ReqWork w = req_work(a, r);
-      const int len = seg_units(a, w);
-      v = (long long)len * a.hkv * w.rgroups;
-      if (cuttable(a, w)) nmax = max(nmax, len);
+      w = req_work(a, r);
+      const int units = seg_units(a, w);
+      v = (long long)units * a.hkv * w.rgroups;
+      if (cuttable(a, w)) len = units;
     }
-    if (c < PLAN_CACHE) u[c] = v;
-    tot += v;
-  }
-#pragma unroll
-  for (int o = 32; o; o >>= 1) {
-    tot += __shfl_xor(tot, o, WAVE);
-    nmax = max(nmax, __shfl_xor(nmax, o, WAVE));
+    if (c < PLAN_CACHE) {
+      u[c] = v; tk[c] = w.tok; ql[c] = w.qlen; ln[c] = w.len;
+    }
+    tot += lane_value64(wave_incl_sum64(v, lane), WAVE - 1);
+    nmax = max(nmax, __builtin_amdgcn_readlane(wave_incl_max(len), WAVE - 1));
   }
   Plan p;
-  p.total = uniform64(tot);
+  p.total = tot;
   long long ch = (p.total + a.workers - 1) / a.workers;
   if (nmax > 0) {
     ch = max(ch, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
@@ -592,27 +639,32 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
   long long base = 0;
   r_out = a.num_seqs;
   start_out = p.total;
+  w_out = ReqWork{0, 0, 0, 0, 0};
   for (int c = 0; c * WAVE < a.num_seqs && pos < p.total; ++c) {
     const int r = c * WAVE + lane;
     long long v = 0;
+    ReqWork w{0, 0, 0, 0, 0};
     if (c < PLAN_CACHE) {
       v = u[c];
+      w.tok = tk[c]; w.qlen = ql[c]; w.len = ln[c];
     } else if (r < a.num_seqs) {
-      const ReqWork w = req_work(a, r);
+      w = req_work(a, r);
       v = (long long)seg_units(a, w) * a.hkv * w.rgroups;
     }
-    long long incl = v;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-      const long long y = __shfl_up(incl, o, WAVE);
-      if (lane >= o) incl += y;
-    }
-    const long long ctot = uniform64(__shfl(incl, WAVE - 1, WAVE));
+    const long long incl = wave_incl_sum64(v, lane);
+    const long long ctot = lane_value64(incl, WAVE - 1);
     if (base + ctot > pos) {
       const unsigned long long m = __ballot(base + incl > pos);
       const int idx = __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
       r_out = c * WAVE + idx;
-      start_out = base + uniform64(__shfl(incl - v, idx, WAVE));
+      start_out = base + lane_value64(incl - v, idx);
+      ReqWork f;
+      f.tok = __builtin_amdgcn_readlane(w.tok, idx);
+      f.qlen = __builtin_amdgcn_readlane(w.qlen, idx);
+      f.len = __builtin_amdgcn_readlane(w.len, idx);
+      f.ntiles = max(1, (f.len + TILE - 1) / TILE);
+      f.rgroups = ((f.qlen * a.G + 15) / 16 + a.rt - 1) / a.rt;
+      w_out = f;
       break;
     }
     base += ctot;
@@ -675,7 +727,7 @@ constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference
 // bf16 out, a cut one an fp32 partial. Every wavefront of the workgroup calls this for every piece
 // (inactive ones -- row tiles past the request's rows -- only join the barriers of the merge).
 template <int D, int PF, bool SHARED>
-__device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
+__device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int tok, int qlen, int seqlen, int kvh, int row0,
                                                int c_begin, int c_end, int ks, int KS, int rtile, bool active,
                                                int part, int nparts, float* lds, int lane) {
   constexpr int KPL = D / 4;        // K bytes per lane and key
@@ -698,7 +750,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   KS = __builtin_amdgcn_readfirstlane(KS);
   const int n = lane & 15, g = lane >> 4;
   const int G = a.G;
-  const int L = a.seq_lens[seq];
+  const int L = __builtin_amdgcn_readfirstlane(seqlen);
   // no keys (malformed): nothing is read. A wavefront with no rows reads nothing either -- except
   // with a shared LDS ring, where it still fetches its share of every tile and keeps the barriers
   constexpr bool shared = SHARED;  // launched with a.lds_ring set
@@ -1246,11 +1298,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   if (worker >= a.workers) return;
   int r;
   long long rstart;
-  const Plan pl = plan_and_locate(a, worker, lane, r, rstart);
+  ReqWork w;
+  const Plan pl = plan_and_locate(a, worker, lane, r, rstart, w);
   long long pos = (long long)worker * pl.chunk;
   const long long end = min(pos + pl.chunk, pl.total);
   if (pos >= end || r >= a.num_seqs) return;
-  ReqWork w = req_work(a, r);
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
   bool whole = !cuttable(a, w);
@@ -1274,11 +1326,11 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     if (c1 <= c0) {
       // fixed-cost units only: nothing to stream here (uniform across the workgroup)
     } else if (a.ksplit > 1 && c1 - c0 >= a.ksplit * COOP_TILES) {
-      attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
+      attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, kspl, a.ksplit, rtile, row0 < w.qlen * a.G,
                             (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
     } else {
       if (solo % a.ksplit == kspl)
-        attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, 0, 1, rtile, row0 < w.qlen * a.G,
+        attend_segment<D, PF, SHARED>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, 0, 1, rtile, row0 < w.qlen * a.G,
                               (int)(worker - first), (int)(last - first + 1), merge_lds, lane);
       ++solo;
     }
@@ -1359,7 +1411,7 @@ __device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (
 // channels (int8_ref's q_gran "group32"): QK step s then holds exactly group s's channels, its integer
 // dot is scaled by that group's q scale and the groups' scores are summed in fp32.
 template <int D, int PF, int QG>
-__device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int tok, int qlen, int kvh, int row0,
+__device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int tok, int qlen, int seqlen, int kvh, int row0,
                                               int c_begin, int c_end, int wave, bool active, int part, int nparts,
                                               uint8_t* ring, int lane) {
   constexpr int KST = D / 32;       // 32-channel QK steps = 32-channel PV tiles
@@ -1380,7 +1432,7 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   wave = __builtin_amdgcn_readfirstlane(wave);
   const int n = lane & 31, h = lane >> 5;
   const int G = a.G;
-  const int L = a.seq_lens[seq];
+  const int L = __builtin_amdgcn_readfirstlane(seqlen);
   // both wavefronts run every tile (they fill the ring together and meet at one barrier per tile)
   if (L <= 0) c_end = c_begin;
   const int nt = c_end - c_begin;
@@ -1401,13 +1453,18 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
     voff[u] = (uint32_t)(rb * (int)a.v_sn + 16 * (pc ^ swz_v<CHR>(row)));
   }
   const int64_t kstep = (int64_t)RPI * a.k_sn, vstep = (int64_t)RPI * a.v_sn;
-  auto dma = [&](int c, int st) {
-    // the half's first key; a half past the end re-reads the tile's first half (an in-bounds page)
-    int key0 = c * TILE + 16 * wave;
-    key0 = key0 < L ? key0 : c * TILE;
-    const int idx = __builtin_amdgcn_readfirstlane(key0 >> a.lbs);
-    int p = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[idx]);
-    p = (p >= 0 && p < a.num_blocks) ? p : 0;
+  // the half's first key; a half past the end re-reads the tile's first half (an in-bounds page)
+  auto half_key = [&](int c) {
+    const int key0 = c * TILE + 16 * wave;
+    return key0 < L ? key0 : c * TILE;
+  };
+  auto page_of = [&](int c) {  // a scalar load of the block table
+    const int idx = __builtin_amdgcn_readfirstlane(half_key(c) >> a.lbs);
+    const int p = __builtin_amdgcn_readfirstlane(((const __attribute__((address_space(4))) int*)bt)[idx]);
+    return (p >= 0 && p < a.num_blocks) ? p : 0;
+  };
+  auto dma_page = [&](int c, int st, int p) {
+    const int key0 = half_key(c);
     const int o = key0 & (bs - 1);
     const int8_t* kb = kbase + (int64_t)p * a.k_sb + (int64_t)o * a.k_sn;
     const int8_t* vb = vbase + (int64_t)p * a.v_sb + (int64_t)o * a.v_sn;
@@ -1421,11 +1478,8 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
                                        0, 0);
     }
   };
+  auto dma = [&](int c, int st) { dma_page(c, st, page_of(c)); };
   constexpr int NIW = 2 * IPH;   // DMA instructions per wavefront and tile
-  if (nt > 0) {
-#pragma unroll
-    for (int j = 0; j < PF - 1; ++j) dma(c_begin + min(j, nt - 1), j);
-  }
 
   // ---- LDS read addresses (slot 0; a slot adds st * SLOT): K of QK step s for lane (key n, half h):
   // logical chunk 2 s + h of row n; V^T of channel tile c, read t: 16-lane group q = lane / 16,
@@ -1449,22 +1503,52 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   }
 
   // ---- q prologue: lane (row n, half h) holds channels 32 s + 16 h + b of row row0 + n; fold s_k,
-  // one scale per row (the two halves exchange their maxima), quantize ----
+  // one scale per row (the two halves exchange their maxima), quantize. Its loads -- the q row, the K
+  // scales, and the V scales the epilogue reads (staged in this wavefront's LDS slice) -- are issued
+  // before the first tiles' page ids and DMAs: vmcnt counts in issue order, so waiting for them does not
+  // wait for the DMAs, and the three round trips overlap instead of adding up ----
   const int R = row0 + n, rtok = R / G, rh = R % G;
   static_assert(QG == 0 || QG == 32, "q scales per row or per 32 channels");
   i32x4 qop[KST];
   float rs;
   float rsg[QG ? KST : 1];   // per-group score scales (QG): q scale x K scale x softmax scale x log2 e
   int lim;
+  float* vsl = reinterpret_cast<float*>(ring + PF * SLOT) + wave * D;   // this wavefront's V scales
   {
-    float x[16 * KST];
-    float amax = 0.f;
-    if (rtok < qlen && active) {
+    const bool qrow = rtok < qlen && active;
+    u32x4 qw[2 * KST];
+    float4 kf[4 * KST];
+    if (qrow) {
       const uint16_t* qp = a.q + (int64_t)(tok + rtok) * a.q_st + (int64_t)(kvh * G + rh) * a.q_sh + 16 * h;
 #pragma unroll
       for (int s = 0; s < KST; ++s) {
-        const u32x4 w0 = *reinterpret_cast<const u32x4*>(qp + 32 * s);
-        const u32x4 w1 = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8);
+        qw[2 * s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
+        qw[2 * s + 1] = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8);
+      }
+      if (a.ks_pc) {
+        const float* kp = a.ks + kvh * D + 16 * h;
+#pragma unroll
+        for (int s = 0; s < KST; ++s)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) kf[4 * s + u] = *reinterpret_cast<const float4*>(kp + 32 * s + 4 * u);
+      }
+    }
+    float2 vs2 = {0.f, 0.f};
+    if (a.vs_pc && 2 * lane < D) vs2 = *reinterpret_cast<const float2*>(a.vs + kvh * D + 2 * lane);
+    if (nt > 0) {
+      int pg[PF - 1];
+#pragma unroll
+      for (int j = 0; j < PF - 1; ++j) pg[j] = page_of(c_begin + min(j, nt - 1));
+#pragma unroll
+      for (int j = 0; j < PF - 1; ++j) dma_page(c_begin + min(j, nt - 1), j, pg[j]);
+    }
+    if (a.vs_pc && 2 * lane < D) *reinterpret_cast<float2*>(vsl + 2 * lane) = vs2;
+    float x[16 * KST];
+    float amax = 0.f;
+    if (qrow) {
+#pragma unroll
+      for (int s = 0; s < KST; ++s) {
+        const u32x4 w0 = qw[2 * s], w1 = qw[2 * s + 1];
         const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -1473,12 +1557,11 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
         }
       }
       if (a.ks_pc) {
-        const float* kp = a.ks + kvh * D + 16 * h;
 #pragma unroll
         for (int s = 0; s < KST; ++s)
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const float4 f = *reinterpret_cast<const float4*>(kp + 32 * s + 4 * u);
+            const float4 f = kf[4 * s + u];
             x[16 * s + 4 * u] *= f.x; x[16 * s + 4 * u + 1] *= f.y;
             x[16 * s + 4 * u + 2] *= f.z; x[16 * s + 4 * u + 3] *= f.w;
           }
@@ -1679,25 +1762,39 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
     const int lim_lo = L - qlen + 1 + row0 / G;          // every row of this wavefront sees keys < lim_lo
     const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
     const int j_full = work ? max(0, min(nt, full_end - c_begin)) : nt;
-    auto step = [&](auto masked_t, int j, auto st_t) {
-      wait_vm<(PF - 2) * NIW>();
+    // Whole rounds keep PF - 2 tiles in flight behind the one they wait for. The last PF - 1 steps issue
+    // no more DMAs (there is nothing left to fetch) and wait for exactly what is still in flight: tile
+    // groups g_0 .. g_{PF-2} came from the prologue (tiles past the end re-read the last one), step j
+    // issued g_{j+PF-1} while j + PF - 1 < nt, so behind tile j there are
+    // ahead = min(PF - 2, max(PF - 2, nt - 1) - j) groups.
+    auto step = [&](auto masked_t, auto tail_t, int j, auto st_t) {
+      if constexpr (decltype(tail_t)::value) {
+        const int ahead = min(PF - 2, max(PF - 2, nt - 1) - j);
+        if (ahead <= 0) wait_vm<0>();
+        else if (ahead == 1) wait_vm<NIW>();
+        else wait_vm<(PF - 2) * NIW>();
+      } else {
+        wait_vm<(PF - 2) * NIW>();
+      }
       lds_barrier();
-      dma(c_begin + min(j + PF - 1, nt - 1), (j + PF - 1) % PF);
+      if (!decltype(tail_t)::value || j + PF - 1 < nt) dma(c_begin + j + PF - 1, (j + PF - 1) % PF);
       if (work) {
         if constexpr (std::is_same_v<decltype(st_t), int>) tile(masked_t, (int)(st_t * SLOT), c_begin + j);
         else tile(masked_t, std::integral_constant<int, decltype(st_t)::value * SLOT>{}, c_begin + j);
       }
     };
     int j = 0;
-    for (; j + PF <= j_full; j += PF) {
-      step(std::false_type{}, j, std::integral_constant<int, 0>{});
-      if constexpr (PF > 1) step(std::false_type{}, j + 1, std::integral_constant<int, 1 % PF>{});
-      if constexpr (PF > 2) step(std::false_type{}, j + 2, std::integral_constant<int, 2 % PF>{});
-      if constexpr (PF > 3) step(std::false_type{}, j + 3, std::integral_constant<int, 3 % PF>{});
+    // whole rounds end at least PF - 1 tiles before nt, so every step of them fetches a real tile
+    const int j_round = min(j_full, nt - (PF - 1));
+    for (; j + PF <= j_round; j += PF) {
+      step(std::false_type{}, std::false_type{}, j, std::integral_constant<int, 0>{});
+      if constexpr (PF > 1) step(std::false_type{}, std::false_type{}, j + 1, std::integral_constant<int, 1 % PF>{});
+      if constexpr (PF > 2) step(std::false_type{}, std::false_type{}, j + 2, std::integral_constant<int, 2 % PF>{});
+      if constexpr (PF > 3) step(std::false_type{}, std::false_type{}, j + 3, std::integral_constant<int, 3 % PF>{});
       static_assert(PF >= 2 && PF <= 4, "rounds are written for 2 to 4 slots");
     }
-    for (; j < j_full; ++j) step(std::false_type{}, j, j % PF);
-    for (; j < nt; ++j) step(std::true_type{}, j, j % PF);
+    for (; j < j_full; ++j) step(std::false_type{}, std::true_type{}, j, j % PF);
+    for (; j < nt; ++j) step(std::true_type{}, std::true_type{}, j, j % PF);
     wait_vm<0>();   // the ring is empty and read before the next piece refills it
     lds_barrier();
   }
@@ -1710,9 +1807,9 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   if (!active || rtok >= qlen) return;
   const int head = kvh * G + rh;
   const int qt = tok + rtok;
-  // the V scales of channels 32 c + 8 j + 4 h .. + 3, fetched next to their use
+  // the V scales of channels 32 c + 8 j + 4 h .. + 3, from the copy the prologue staged in LDS
   auto vscale4 = [&](int c, int j) -> float4 {
-    if (a.vs_pc) return *reinterpret_cast<const float4*>(a.vs + kvh * D + 32 * c + 8 * j + 4 * h);
+    if (a.vs_pc) return *reinterpret_cast<const float4*>(vsl + 32 * c + 8 * j + 4 * h);
     const float v = a.vs[kvh];
     return float4{v, v, v, v};
   };
@@ -1762,11 +1859,11 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
   if (worker >= a.workers) return;
   int r;
   long long rstart;
-  const Plan pl = plan_and_locate(a, worker, lane, r, rstart);
+  ReqWork w;
+  const Plan pl = plan_and_locate(a, worker, lane, r, rstart, w);
   long long pos = (long long)worker * pl.chunk;
   const long long end = min(pos + pl.chunk, pl.total);
   if (pos >= end || r >= a.num_seqs) return;
-  ReqWork w = req_work(a, r);
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
   bool whole = !cuttable(a, w);
@@ -1782,7 +1879,7 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
     const int c0 = whole ? 0 : max(off - fc, 0);
     const int c1 = whole ? (off == 0 ? w.ntiles : 0) : max(off + take - fc, 0);
     if (c1 > c0)
-      attend_rows32<D, PF, QG>(a, r, w.tok, w.qlen, kvh, row0, c0, c1, wave, row0 < w.qlen * a.G, (int)(worker - first),
+      attend_rows32<D, PF, QG>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, wave, row0 < w.qlen * a.G, (int)(worker - first),
                            (int)(last - first + 1), ring, lane);
     pos += take;
     off = 0;
@@ -3022,8 +3119,10 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;
   a.seg_cost = seg_cost_units(a.lds_ring != 0);
   const int pf = rows32 ? v32_ring_depth() : a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
-  const size_t lds = a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
-                                : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
+  // rows32: the ring, then each wavefront's V scales
+  const size_t lds = rows32     ? (size_t)pf * 2 * TILE * head_dim + (size_t)V32_WAVES * head_dim * sizeof(float)
+                     : a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
+                                  : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
   void (*kern)(AttnArgs);
   if (rows32) {
     if (q_group == 32) {
