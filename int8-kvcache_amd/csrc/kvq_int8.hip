@@ -60,6 +60,7 @@ constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kern
                                                // one ring): verification batches time best at 12
 constexpr int DEFAULT_PREFETCH = 3;
 constexpr int DEFAULT_V32_RING = 3;     // verify_kernel's ring slots
+constexpr int DEFAULT_V32_KSPLIT = 2;   // verify_kernel's key splits per workgroup
 constexpr int NUM_XCDS = 8;
 
 // ------------------------------------------------------------------------------------------------
@@ -1351,9 +1352,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 
 // ------------------------------------------------------------------------------------------------
 // Verification-shape attention: more than 32 (token, q head) rows per (request, kv head), e.g. 8
-// speculative tokens x 7 q heads = 56 rows. A workgroup of 2 wavefronts takes a piece of one (request,
-// kv head, group of 64 rows); wavefront w owns rows row0 = 32 w .. 32 w + 31 of the group and the two
-// share each 32-key K/V tile through an LDS ring (wavefront w DMAs keys 16 w .. 16 w + 15 of it).
+// speculative tokens x 7 q heads = 56 rows. A workgroup of 2 x KS wavefronts takes a piece of one
+// (request, kv head, group of 64 rows): row wavefront rw owns rows row0 = 32 rw .. 32 rw + 31 of the
+// group, key split kw streams the piece's tiles kw, kw + KS, ...; the two row wavefronts of a key split
+// share each 32-key K/V tile through the split's LDS ring (wavefront rw DMAs keys 16 rw .. 16 rw + 15 of
+// it), and at the end of the piece key split 1 hands its running max, denominator and accumulators to
+// key split 0 through LDS. Two key splits halve the pieces a batch is cut into at the same wavefront
+// count -- and with them the fixed cost per piece (q prologue, first DMAs, finish) and the fp32 partials
+// the merge kernel reads (c3: 68.8 -> 66.1 us).
 // Per tile and wavefront, on the 32x32 int8 MFMA (lane l: n = l % 32, h = l / 32):
 //   QK  S^T[key][row] = K . Q^T   v_mfma_i32_32x32x32_i8 x D/32, A = K (lane: key n, channel half h of
 //       each 32-channel step), B = Q^T (lane: row n, same channels)
@@ -1371,7 +1377,6 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // row, doubled) so that the K reads (16 rows, one chunk) and the transposing V reads (8 rows x 2
 // chunks per 16 lanes) fall on distinct banks.
 // ------------------------------------------------------------------------------------------------
-constexpr int V32_WAVES = 2;      // wavefronts per workgroup (32 rows each)
 constexpr int V32_GROUP_TILES = 4;  // 16-row tiles per row group (the stream-K plan's unit of rows)
 
 template <int CHR>
@@ -1410,10 +1415,10 @@ __device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (
 // QG: 0 = one q scale per (token, q head) row (implementation B's per-token-head q); 32 = one per 32
 // channels (int8_ref's q_gran "group32"): QK step s then holds exactly group s's channels, its integer
 // dot is scaled by that group's q scale and the groups' scores are summed in fp32.
-template <int D, int PF, int QG>
+template <int D, int PF, int QG, int KS>
 __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int tok, int qlen, int seqlen, int kvh, int row0,
-                                              int c_begin, int c_end, int wave, bool active, int part, int nparts,
-                                              uint8_t* ring, int lane) {
+                                              int c_begin, int c_end, int wave, int kw, bool active, int part,
+                                              int nparts, uint8_t* ring, float* vsl, float* merge, int lane) {
   constexpr int KST = D / 32;       // 32-channel QK steps = 32-channel PV tiles
   constexpr int CHR = D / 16;       // 16-byte chunks per K (or V) row
   constexpr int RPI = WAVE / CHR;   // rows per DMA instruction
@@ -1430,12 +1435,18 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   part = __builtin_amdgcn_readfirstlane(part);
   nparts = __builtin_amdgcn_readfirstlane(nparts);
   wave = __builtin_amdgcn_readfirstlane(wave);
+  kw = __builtin_amdgcn_readfirstlane(kw);
   const int n = lane & 31, h = lane >> 5;
   const int G = a.G;
   const int L = __builtin_amdgcn_readfirstlane(seqlen);
-  // both wavefronts run every tile (they fill the ring together and meet at one barrier per tile)
+  // key split kw takes the piece's tiles kw, kw + KS, ...: ntk of them, in nsteps steps (the same count
+  // for every wavefront of the workgroup -- a split with fewer tiles ends with an empty step); the two
+  // wavefronts of a split fill its ring together, and all meet at one barrier per step
   if (L <= 0) c_end = c_begin;
   const int nt = c_end - c_begin;
+  const int ntk = nt > kw ? (nt - kw + KS - 1) / KS : 0;
+  const int nsteps = (nt + KS - 1) / KS;
+  auto tile_of = [&](int i) { return c_begin + kw + i * KS; };   // the split's i-th tile
   const bool work = L > 0 && active;
   const int* bt = a.block_table + (int64_t)seq * a.bt_stride;
   const int bs = 1 << a.lbs;
@@ -1513,7 +1524,6 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   float rs;
   float rsg[QG ? KST : 1];   // per-group score scales (QG): q scale x K scale x softmax scale x log2 e
   int lim;
-  float* vsl = reinterpret_cast<float*>(ring + PF * SLOT) + wave * D;   // this wavefront's V scales
   {
     const bool qrow = rtok < qlen && active;
     u32x4 qw[2 * KST];
@@ -1534,15 +1544,16 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
       }
     }
     float2 vs2 = {0.f, 0.f};
-    if (a.vs_pc && 2 * lane < D) vs2 = *reinterpret_cast<const float2*>(a.vs + kvh * D + 2 * lane);
+    if (kw == 0 && a.vs_pc && 2 * lane < D) vs2 = *reinterpret_cast<const float2*>(a.vs + kvh * D + 2 * lane);
     if (nt > 0) {
+      // groups past the split's last tile re-read the piece's last tile (in bounds, never read back)
       int pg[PF - 1];
 #pragma unroll
-      for (int j = 0; j < PF - 1; ++j) pg[j] = page_of(c_begin + min(j, nt - 1));
+      for (int j = 0; j < PF - 1; ++j) pg[j] = page_of(min(tile_of(j), c_end - 1));
 #pragma unroll
-      for (int j = 0; j < PF - 1; ++j) dma_page(c_begin + min(j, nt - 1), j, pg[j]);
+      for (int j = 0; j < PF - 1; ++j) dma_page(min(tile_of(j), c_end - 1), j, pg[j]);
     }
-    if (a.vs_pc && 2 * lane < D) *reinterpret_cast<float2*>(vsl + 2 * lane) = vs2;
+    if (kw == 0 && a.vs_pc && 2 * lane < D) *reinterpret_cast<float2*>(vsl + 2 * lane) = vs2;
     float x[16 * KST];
     float amax = 0.f;
     if (qrow) {
@@ -1753,23 +1764,25 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
     }
   };
 
-  // ---- main loop: one barrier per tile. Tile j sits in slot j % PF; after the barrier (this
-  // wavefront's DMA of tile j has landed, everyone's has, and everyone is done with tile j - 1) slot
-  // (j + PF - 1) % PF takes tile j + PF - 1. Tiles j < j_full have no masked key for any row of this
-  // wavefront (a loop of whole rounds of PF of them, with compile-time slots, then the rest); the two
-  // wavefronts may split their tiles differently but each meets exactly one barrier per tile. ----
+  // ---- main loop: one barrier per step. The split's i-th tile sits in slot i % PF of its ring; after
+  // the barrier (this wavefront's DMA of it has landed, everyone's has, and everyone is done with step
+  // i - 1) slot (i + PF - 1) % PF takes the split's tile i + PF - 1. Tiles before j_full (piece-relative)
+  // have no masked key for any row of this wavefront (a loop of whole rounds of PF of them, with
+  // compile-time slots, then the rest); wavefronts may split their steps differently between the loops
+  // but each meets exactly nsteps barriers. ----
   if (nt > 0) {
     const int lim_lo = L - qlen + 1 + row0 / G;          // every row of this wavefront sees keys < lim_lo
     const int full_end = lim_lo > 0 ? lim_lo / TILE : 0;
     const int j_full = work ? max(0, min(nt, full_end - c_begin)) : nt;
-    // Whole rounds keep PF - 2 tiles in flight behind the one they wait for. The last PF - 1 steps issue
-    // no more DMAs (there is nothing left to fetch) and wait for exactly what is still in flight: tile
-    // groups g_0 .. g_{PF-2} came from the prologue (tiles past the end re-read the last one), step j
-    // issued g_{j+PF-1} while j + PF - 1 < nt, so behind tile j there are
-    // ahead = min(PF - 2, max(PF - 2, nt - 1) - j) groups.
-    auto step = [&](auto masked_t, auto tail_t, int j, auto st_t) {
+    const int i_full = j_full > kw ? (j_full - kw + KS - 1) / KS : 0;   // the split's unmasked tiles
+    // Whole rounds keep PF - 2 of the split's tiles in flight behind the one they wait for. The last
+    // PF - 1 steps issue no more DMAs and wait for exactly what is still in flight: groups g_0 .. g_{PF-2}
+    // came from the prologue (past the split's end: re-reads), step i issued g_{i+PF-1} while
+    // i + PF - 1 < ntk, so behind the split's tile i there are ahead = min(PF - 2, max(PF - 2, ntk - 1) - i)
+    // groups; a step past the split's tiles (i >= ntk) only waits and meets the barrier.
+    auto step = [&](auto masked_t, auto tail_t, int i, auto st_t) {
       if constexpr (decltype(tail_t)::value) {
-        const int ahead = min(PF - 2, max(PF - 2, nt - 1) - j);
+        const int ahead = min(PF - 2, max(PF - 2, ntk - 1) - i);
         if (ahead <= 0) wait_vm<0>();
         else if (ahead == 1) wait_vm<NIW>();
         else wait_vm<(PF - 2) * NIW>();
@@ -1777,24 +1790,24 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
         wait_vm<(PF - 2) * NIW>();
       }
       lds_barrier();
-      if (!decltype(tail_t)::value || j + PF - 1 < nt) dma(c_begin + j + PF - 1, (j + PF - 1) % PF);
-      if (work) {
-        if constexpr (std::is_same_v<decltype(st_t), int>) tile(masked_t, (int)(st_t * SLOT), c_begin + j);
-        else tile(masked_t, std::integral_constant<int, decltype(st_t)::value * SLOT>{}, c_begin + j);
+      if (!decltype(tail_t)::value || i + PF - 1 < ntk) dma(tile_of(i + PF - 1), (i + PF - 1) % PF);
+      if (work && (!decltype(tail_t)::value || i < ntk)) {
+        if constexpr (std::is_same_v<decltype(st_t), int>) tile(masked_t, (int)(st_t * SLOT), tile_of(i));
+        else tile(masked_t, std::integral_constant<int, decltype(st_t)::value * SLOT>{}, tile_of(i));
       }
     };
-    int j = 0;
-    // whole rounds end at least PF - 1 tiles before nt, so every step of them fetches a real tile
-    const int j_round = min(j_full, nt - (PF - 1));
-    for (; j + PF <= j_round; j += PF) {
-      step(std::false_type{}, std::false_type{}, j, std::integral_constant<int, 0>{});
-      if constexpr (PF > 1) step(std::false_type{}, std::false_type{}, j + 1, std::integral_constant<int, 1 % PF>{});
-      if constexpr (PF > 2) step(std::false_type{}, std::false_type{}, j + 2, std::integral_constant<int, 2 % PF>{});
-      if constexpr (PF > 3) step(std::false_type{}, std::false_type{}, j + 3, std::integral_constant<int, 3 % PF>{});
+    int i = 0;
+    // whole rounds end at least PF - 1 tiles before the split's end, so every step of them fetches a real tile
+    const int i_round = min(i_full, ntk - (PF - 1));
+    for (; i + PF <= i_round; i += PF) {
+      step(std::false_type{}, std::false_type{}, i, std::integral_constant<int, 0>{});
+      if constexpr (PF > 1) step(std::false_type{}, std::false_type{}, i + 1, std::integral_constant<int, 1 % PF>{});
+      if constexpr (PF > 2) step(std::false_type{}, std::false_type{}, i + 2, std::integral_constant<int, 2 % PF>{});
+      if constexpr (PF > 3) step(std::false_type{}, std::false_type{}, i + 3, std::integral_constant<int, 3 % PF>{});
       static_assert(PF >= 2 && PF <= 4, "rounds are written for 2 to 4 slots");
     }
-    for (; j < j_full; ++j) step(std::false_type{}, std::true_type{}, j, j % PF);
-    for (; j < nt; ++j) step(std::true_type{}, std::true_type{}, j, j % PF);
+    for (; i < min(i_full, ntk); ++i) step(std::false_type{}, std::true_type{}, i, i % PF);
+    for (; i < nsteps; ++i) step(std::true_type{}, std::true_type{}, i, i % PF);
     wait_vm<0>();   // the ring is empty and read before the next piece refills it
     lds_barrier();
   }
@@ -1803,6 +1816,35 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
     l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
+  if constexpr (KS == 2) {
+    // key split 1 hands its (m, l, acc) to key split 0 of the same rows through LDS (the rings' space,
+    // free now: lane-major [field][lane], conflict-free), which merges them:
+    // M = max(m0, m1), acc = 2^(m0 - M) acc0 + 2^(m1 - M) acc1, l likewise
+    constexpr int MF = 16 * KST + 2;
+    float* mb = merge + (wave & 1) * MF * WAVE + lane;
+    if (kw == 1) {
+#pragma unroll
+      for (int c = 0; c < KST; ++c)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mb[(16 * c + v) * WAVE] = acc[c][v];
+      mb[16 * KST * WAVE] = m;
+      mb[(16 * KST + 1) * WAVE] = l;
+    }
+    lds_barrier();
+    if (kw == 0) {
+      const float m1 = mb[16 * KST * WAVE], l1 = mb[(16 * KST + 1) * WAVE];
+      const float M = __builtin_fmaxf(m, m1);
+      const float a0 = __builtin_amdgcn_exp2f(m - M), a1 = __builtin_amdgcn_exp2f(m1 - M);
+#pragma unroll
+      for (int c = 0; c < KST; ++c)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[c][v] = __builtin_fmaf(acc[c][v], a0, mb[(16 * c + v) * WAVE] * a1);
+      l = __builtin_fmaf(l, a0, l1 * a1);
+      m = M;
+    }
+    lds_barrier();   // read before the next piece's DMAs refill the rings
+    if (kw != 0) return;
   }
   if (!active || rtok >= qlen) return;
   const int head = kvh * G + rh;
@@ -1845,11 +1887,19 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
 }
 
 // Stream-K over the batch as attn_kernel (plan_and_locate, the same units and pieces), for row groups
-// of 64 rows run by the 2 wavefronts of attend_rows32.
-template <int D, int PF, int QG>
-__global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
+// of 64 rows run by 2 x KS wavefronts: row wavefront rw = wave % 2 (rows 32 rw .. 32 rw + 31 of the
+// group) of key split kw = wave / 2. Dynamic LDS: KS rings of PF slots, then the V scales of the 2 row
+// wavefronts of key split 0.
+template <int D, int PF, int QG, int KS>
+__global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
-  extern __shared__ float v32_lds[];   // the ring: PF slots of 32 keys' K rows then V rows
+  const int rw = wave & 1, kw = wave >> 1;
+  extern __shared__ float v32_lds[];
+  constexpr int SLOT = 2 * TILE * D;
+  uint8_t* rings = reinterpret_cast<uint8_t*>(v32_lds);
+  uint8_t* ring = rings + kw * PF * SLOT;
+  float* vsl = reinterpret_cast<float*>(rings + KS * PF * SLOT) + rw * D;
+  float* merge = reinterpret_cast<float*>(rings);
   int worker = blockIdx.x;
   if (a.xcd_order) {
     const int q = a.workers / NUM_XCDS, rem = a.workers % NUM_XCDS;
@@ -1867,7 +1917,6 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
   int seglen = seg_units(a, w);
   int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
   bool whole = !cuttable(a, w);
-  uint8_t* ring = reinterpret_cast<uint8_t*>(v32_lds);
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
     const int take = (int)min((long long)(seglen - off), end - pos);
@@ -1875,12 +1924,12 @@ __global__ __launch_bounds__(WAVE * V32_WAVES) void verify_kernel(AttnArgs a) {
     const long long first = whole ? worker : (seg_start + fc) / pl.chunk;
     const long long last = whole ? worker : (seg_start + seglen - 1) / pl.chunk;
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
-    const int row0 = rg * (16 * V32_GROUP_TILES) + 32 * wave;
+    const int row0 = rg * (16 * V32_GROUP_TILES) + 32 * rw;
     const int c0 = whole ? 0 : max(off - fc, 0);
     const int c1 = whole ? (off == 0 ? w.ntiles : 0) : max(off + take - fc, 0);
     if (c1 > c0)
-      attend_rows32<D, PF, QG>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, wave, row0 < w.qlen * a.G, (int)(worker - first),
-                           (int)(last - first + 1), ring, lane);
+      attend_rows32<D, PF, QG, KS>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, rw, kw, row0 < w.qlen * a.G,
+                                   (int)(worker - first), (int)(last - first + 1), ring, vsl, merge, lane);
     pos += take;
     off = 0;
     if (++seg == a.hkv * w.rgroups && pos < end) {  // on to the next request with work
@@ -2645,14 +2694,18 @@ int log2i(int64_t x) {
 }
 // Work units (32-key tiles of one workgroup's streaming) charged per segment for its fixed cost in
 // the stream-K partition, per kernel (KVQ_SEG_COST overrides both)
-int seg_cost_units(bool lds_ring) {
+int seg_cost_units(bool lds_ring, int v32_key_splits) {
   static const int env = [] {
     const char* e = getenv("KVQ_SEG_COST");
     if (!e) return -1;
     const int v = atoi(e);
     return v < 0 ? 0 : (v > 64 ? 64 : v);
   }();
-  return env >= 0 ? env : (lds_ring ? DEFAULT_SEG_COST_LDS_RING : DEFAULT_SEG_COST);
+  // verify_kernel with 2 key splits streams a unit (one 32-key tile of the segment) in half the time, so
+  // its fixed cost is twice the units (c3: 12 -> 24 units 68.5 -> 66.1 us; 36 units 67.3, 48 units 71.3)
+  if (env >= 0) return env;
+  if (v32_key_splits == 2) return 2 * DEFAULT_SEG_COST_LDS_RING;
+  return lds_ring ? DEFAULT_SEG_COST_LDS_RING : DEFAULT_SEG_COST;
 }
 
 // slots of the attention's shared LDS ring (KVQ_LDS_PREFETCH: 3, 4 or 6)
@@ -2671,6 +2724,12 @@ int v32_ring_depth() {
   const char* e = getenv("KVQ_V32_RING");
   const int v = e ? atoi(e) : DEFAULT_V32_RING;
   return v <= 3 ? 3 : 4;
+}
+// verify_kernel's key splits per workgroup (KVQ_V32_KSPLIT: 1 or 2)
+int v32_key_splits() {
+  const char* e = getenv("KVQ_V32_KSPLIT");
+  const int v = e ? atoi(e) : DEFAULT_V32_KSPLIT;
+  return v <= 1 ? 1 : 2;
 }
 
 // Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
@@ -3092,7 +3151,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   // (per-32-channel q scales run there for every row count)
   const bool rows32 = q_group == 32 ||
                       ((int64_t)G * maxq > 32 && !(getenv("KVQ_ROWS32") && atoi(getenv("KVQ_ROWS32")) == 0));
-  const int waves = rows32 ? V32_WAVES : rt * ks;
+  const int v32ks = rows32 ? v32_key_splits() : 1;
+  const int waves = rows32 ? 2 * v32ks : rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535 || (num_q_heads + RED_WAVES - 1) / RED_WAVES > 65535 ||
       maxq > 65535)
     return fail("int8_decode_attention: grid too large");
@@ -3111,27 +3171,31 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.num_seqs = (int)num_seqs; a.hkv = (int)num_kv_heads;
   a.max_splits = (int)num_splits;
   a.cut_rows = num_splits > 1 ? (int)std::min<int64_t>(segm_rows, INT32_MAX) : 0;
-  a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? 1 : ks; a.waves = waves;
+  a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? v32ks : ks; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES * a.ksplit;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
   a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;
-  a.seg_cost = seg_cost_units(a.lds_ring != 0);
+  a.seg_cost = seg_cost_units(a.lds_ring != 0, rows32 ? v32ks : 0);
   const int pf = rows32 ? v32_ring_depth() : a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
-  // rows32: the ring, then each wavefront's V scales
-  const size_t lds = rows32     ? (size_t)pf * 2 * TILE * head_dim + (size_t)V32_WAVES * head_dim * sizeof(float)
+  // rows32: a ring per key split, then the V scales of key split 0's two row wavefronts (the key-split
+  // merge reuses the rings: 2 x (16 D / 32 + 2) x 64 floats, less than one ring of 3 slots)
+  const size_t lds = rows32     ? (size_t)v32ks * pf * 2 * TILE * head_dim + (size_t)2 * head_dim * sizeof(float)
                      : a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
                                   : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
   void (*kern)(AttnArgs);
   if (rows32) {
-    if (q_group == 32) {
-      if (head_dim == 128) kern = pf == 3 ? verify_kernel<128, 3, 32> : verify_kernel<128, 4, 32>;
-      else kern = pf == 3 ? verify_kernel<64, 3, 32> : verify_kernel<64, 4, 32>;
-    } else {
-      if (head_dim == 128) kern = pf == 3 ? verify_kernel<128, 3, 0> : verify_kernel<128, 4, 0>;
-      else kern = pf == 3 ? verify_kernel<64, 3, 0> : verify_kernel<64, 4, 0>;
-    }
+    auto pick = [&](auto qg_t) -> void (*)(AttnArgs) {
+      constexpr int QG = decltype(qg_t)::value;
+      if (head_dim == 128) {
+        if (v32ks == 2) return pf == 3 ? verify_kernel<128, 3, QG, 2> : verify_kernel<128, 4, QG, 2>;
+        return pf == 3 ? verify_kernel<128, 3, QG, 1> : verify_kernel<128, 4, QG, 1>;
+      }
+      if (v32ks == 2) return pf == 3 ? verify_kernel<64, 3, QG, 2> : verify_kernel<64, 4, QG, 2>;
+      return pf == 3 ? verify_kernel<64, 3, QG, 1> : verify_kernel<64, 4, QG, 1>;
+    };
+    kern = q_group == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
   } else if (a.lds_ring) {
     if (head_dim == 128) kern = pf == 3 ? attn_kernel<128, 3, true> : pf == 6 ? attn_kernel<128, 6, true> : attn_kernel<128, 4, true>;
     else kern = pf == 3 ? attn_kernel<64, 3, true> : pf == 6 ? attn_kernel<64, 6, true> : attn_kernel<64, 4, true>;
