@@ -59,8 +59,9 @@ constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: 
 constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kernel (4 row tiles filling
                                                // one ring): verification batches time best at 12
 constexpr int DEFAULT_PREFETCH = 3;
-constexpr int DEFAULT_V32_RING = 3;     // verify_kernel's ring slots
+constexpr int DEFAULT_V32_RING = 2;     // verify_kernel's ring slots (3 with one key split)
 constexpr int DEFAULT_V32_KSPLIT = 2;   // verify_kernel's key splits per workgroup
+constexpr int DEFAULT_SEG_COST_V32_KS2 = 16;  // fixed cost of a segment in verify_kernel with 2 key splits
 constexpr int NUM_XCDS = 8;
 
 // ------------------------------------------------------------------------------------------------
@@ -692,6 +693,34 @@ __device__ __forceinline__ void wait_vm() {
 // flight (they write LDS), which the rings keep outstanding on purpose.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// code bytes of q: rint(x / s) saturated, from r = rcp(s) with the rounding shortcut of quant8 (exact
+// division for a lane whose quotients come near a half-integer); x holds the lane's N channels. Codes
+// are packed as they are made, so only x and the packed words are live at once.
+template <int N>
+__device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (&out)[N / 4]) {
+  const float r = __builtin_amdgcn_rcpf(s);
+  float worst = 0.f;
+#pragma unroll
+  for (int u = 0; u < N / 4; ++u) {
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float xe = x[4 * u + i];
+      const float t0 = __builtin_fmaf(xe, r, QC_MAGIC);
+      const float res = __builtin_fmaf(xe, r, -(t0 - QC_MAGIC));
+      worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
+      t[i] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
+    }
+    out[u] = pack_magic4(t[0], t[1], t[2], t[3]);
+  }
+  if (worst >= 0.5f - 0x1p-14f) {
+#pragma unroll
+    for (int u = 0; u < N / 4; ++u)
+      out[u] = pack_magic4(code_exact(x[4 * u], s) + QC_MAGIC, code_exact(x[4 * u + 1], s) + QC_MAGIC,
+                           code_exact(x[4 * u + 2], s) + QC_MAGIC, code_exact(x[4 * u + 3], s) + QC_MAGIC);
+  }
+}
+
 template <int D>
 struct KVTile {
   i32x4 k[2][D / 64];     // QK A operands: keys 16b + m, bytes = channels (D/4) g + 16 s + j
@@ -939,6 +968,26 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
   };
 
   KVTile<D> ring[SHARED ? 1 : PF];  // the register ring (unused with the LDS ring)
+  // ---- q prologue, part 1: the q row and its K scales are requested before the first tiles' K/V, so
+  // that waiting for them (vmcnt counts in issue order) does not wait for the tiles, and quantizing q
+  // overlaps the tiles' flight ----
+  const bool qrow = rtok < qlen;
+  u32x4 qraw[KPL / 8];
+  float ksc[KPL];
+  if (qrow) {
+    const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + (int64_t)(tok + rtok) * a.q_st +
+                                                     (int64_t)(kvh * G + rh) * a.q_sh + g * KPL);
+#pragma unroll
+    for (int u = 0; u < KPL / 8; ++u) qraw[u] = qp[u];
+    if (a.ks_pc) {
+      const float4* kp = reinterpret_cast<const float4*>(a.ks + kvh * D + g * KPL);
+#pragma unroll
+      for (int u = 0; u < KPL / 4; ++u) {
+        const float4 f = kp[u];
+        ksc[4 * u] = f.x; ksc[4 * u + 1] = f.y; ksc[4 * u + 2] = f.z; ksc[4 * u + 3] = f.w;
+      }
+    }
+  }
   if (nt > 0) {
     if constexpr (SHARED) {
       with_niw([&](auto niw_t) {
@@ -951,16 +1000,15 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     }
   }
 
-  // ---- q prologue: fold s_k, one scale per row, quantize (exact division) ----
+  // ---- q prologue, part 2: fold s_k, one scale per row, quantize (codes of rint(x / s), the rounding
+  // shortcut of q_codes with exact division where a quotient nears a half-integer) ----
   {
     float x[KPL];
     float amax = 0.f;
-    if (rtok < qlen) {
-      const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + (int64_t)(tok + rtok) * a.q_st +
-                                                       (int64_t)(kvh * G + rh) * a.q_sh + g * KPL);
+    if (qrow) {
 #pragma unroll
       for (int u = 0; u < KPL / 8; ++u) {
-        const u32x4 w = qp[u];
+        const u32x4 w = qraw[u];
         x[8 * u + 0] = bf16_lo(w.x); x[8 * u + 1] = bf16_hi(w.x);
         x[8 * u + 2] = bf16_lo(w.y); x[8 * u + 3] = bf16_hi(w.y);
         x[8 * u + 4] = bf16_lo(w.z); x[8 * u + 5] = bf16_hi(w.z);
@@ -968,7 +1016,7 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
       }
       if (a.ks_pc) {
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) x[e] = x[e] * a.ks[kvh * D + g * KPL + e];
+        for (int e = 0; e < KPL; ++e) x[e] = x[e] * ksc[e];
       }
 #pragma unroll
       for (int e = 0; e < KPL; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[e]));
@@ -978,17 +1026,11 @@ __device__ __forceinline__ void attend_segment(const AttnArgs& a, int seq, int t
     }
     amax = group4_fmax(amax);
     const float s = __builtin_fmaxf(amax / 127.f, 1e-8f);
+    uint32_t codes[KPL / 4];
+    q_codes<KPL>(x, s, codes);
 #pragma unroll
-    for (int st = 0; st < KSTEPS; ++st) {
-      i32x4 w;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int e = 16 * st + 4 * u;
-        w[u] = (int)pack_i8x4(code_exact(x[e], s), code_exact(x[e + 1], s), code_exact(x[e + 2], s),
-                              code_exact(x[e + 3], s));
-      }
-      qop[st] = w;
-    }
+    for (int st = 0; st < KSTEPS; ++st)
+      qop[st] = i32x4{(int)codes[4 * st], (int)codes[4 * st + 1], (int)codes[4 * st + 2], (int)codes[4 * st + 3]};
     rs = s * (a.ks_pc ? 1.f : a.ks[kvh]) * a.sm_log2;
     lim = rtok < qlen ? L - qlen + 1 + rtok : L;  // keys < lim are visible to this row
   }
@@ -1377,40 +1419,20 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 // row, doubled) so that the K reads (16 rows, one chunk) and the transposing V reads (8 rows x 2
 // chunks per 16 lanes) fall on distinct banks.
 // ------------------------------------------------------------------------------------------------
-constexpr int V32_GROUP_TILES = 4;  // 16-row tiles per row group (the stream-K plan's unit of rows)
+constexpr int V32_GROUP_TILES = 4;
+// verify_kernel's dynamic LDS: KS rings of PF slots (K then V rows of 32 keys), which the key-split
+// merge reuses (2 row wavefronts x (16 D / 32 + 2) fields x 64 lanes of fp32) -- at least as large as
+// either -- then the V scales of key split 0's two row wavefronts
+constexpr int64_t v32_vscale_offset(int64_t d, int64_t pf, int64_t ks) {
+  const int64_t rings = ks * pf * 2 * TILE * d, merge = ks == 2 ? 2 * (16 * (d / 32) + 2) * WAVE * 4 : 0;
+  return rings > merge ? rings : merge;
+}
+constexpr int64_t v32_lds_bytes(int64_t d, int64_t pf, int64_t ks) { return v32_vscale_offset(d, pf, ks) + 2 * d * 4; }  // 16-row tiles per row group (the stream-K plan's unit of rows)
 
 template <int CHR>
 __device__ __forceinline__ int swz_k(int row) { return (row >> 1) & (CHR - 1); }
 template <int CHR>
 __device__ __forceinline__ int swz_v(int row) { return ((((row >> 1) & 1) | (((row >> 3) & 1) << 1)) << 1) & (CHR - 1); }
-
-// code bytes of q: rint(x / s) saturated, from r = rcp(s) with the rounding shortcut of quant8 (exact
-// division for a lane whose quotients come near a half-integer); x holds the lane's N channels. Codes
-// are packed as they are made, so only x and the packed words are live at once.
-template <int N>
-__device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (&out)[N / 4]) {
-  const float r = __builtin_amdgcn_rcpf(s);
-  float worst = 0.f;
-#pragma unroll
-  for (int u = 0; u < N / 4; ++u) {
-    float t[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float xe = x[4 * u + i];
-      const float t0 = __builtin_fmaf(xe, r, QC_MAGIC);
-      const float res = __builtin_fmaf(xe, r, -(t0 - QC_MAGIC));
-      worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
-      t[i] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
-    }
-    out[u] = pack_magic4(t[0], t[1], t[2], t[3]);
-  }
-  if (worst >= 0.5f - 0x1p-14f) {
-#pragma unroll
-    for (int u = 0; u < N / 4; ++u)
-      out[u] = pack_magic4(code_exact(x[4 * u], s) + QC_MAGIC, code_exact(x[4 * u + 1], s) + QC_MAGIC,
-                           code_exact(x[4 * u + 2], s) + QC_MAGIC, code_exact(x[4 * u + 3], s) + QC_MAGIC);
-  }
-}
 
 // QG: 0 = one q scale per (token, q head) row (implementation B's per-token-head q); 32 = one per 32
 // channels (int8_ref's q_gran "group32"): QK step s then holds exactly group s's channels, its integer
@@ -1888,7 +1910,7 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
 
 // Stream-K over the batch as attn_kernel (plan_and_locate, the same units and pieces), for row groups
 // of 64 rows run by 2 x KS wavefronts: row wavefront rw = wave % 2 (rows 32 rw .. 32 rw + 31 of the
-// group) of key split kw = wave / 2. Dynamic LDS: KS rings of PF slots, then the V scales of the 2 row
+// group) of key split kw = wave / 2. Dynamic LDS (v32_lds_bytes): KS rings of PF slots, then the V scales of the 2 row
 // wavefronts of key split 0.
 template <int D, int PF, int QG, int KS>
 __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
@@ -1898,7 +1920,7 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
   constexpr int SLOT = 2 * TILE * D;
   uint8_t* rings = reinterpret_cast<uint8_t*>(v32_lds);
   uint8_t* ring = rings + kw * PF * SLOT;
-  float* vsl = reinterpret_cast<float*>(rings + KS * PF * SLOT) + rw * D;
+  float* vsl = reinterpret_cast<float*>(rings + v32_vscale_offset(D, PF, KS)) + rw * D;
   float* merge = reinterpret_cast<float*>(rings);
   int worker = blockIdx.x;
   if (a.xcd_order) {
@@ -2702,9 +2724,10 @@ int seg_cost_units(bool lds_ring, int v32_key_splits) {
     return v < 0 ? 0 : (v > 64 ? 64 : v);
   }();
   // verify_kernel with 2 key splits streams a unit (one 32-key tile of the segment) in half the time, so
-  // its fixed cost is twice the units (c3: 12 -> 24 units 68.5 -> 66.1 us; 36 units 67.3, 48 units 71.3)
+  // its fixed cost is more units (c3, 3-slot rings: 12 -> 24 units 68.5 -> 66.1 us, 36 units 67.3, 48
+  // units 71.3; 2-slot rings: 16 units 65.1-65.3 us, 24 units 66.1-66.9)
   if (env >= 0) return env;
-  if (v32_key_splits == 2) return 2 * DEFAULT_SEG_COST_LDS_RING;
+  if (v32_key_splits == 2) return DEFAULT_SEG_COST_V32_KS2;
   return lds_ring ? DEFAULT_SEG_COST_LDS_RING : DEFAULT_SEG_COST;
 }
 
@@ -2723,7 +2746,7 @@ int lds_prefetch_depth() {
 int v32_ring_depth() {
   const char* e = getenv("KVQ_V32_RING");
   const int v = e ? atoi(e) : DEFAULT_V32_RING;
-  return v <= 3 ? 3 : 4;
+  return v <= 2 ? 2 : v == 3 ? 3 : 4;
 }
 // verify_kernel's key splits per workgroup (KVQ_V32_KSPLIT: 1 or 2)
 int v32_key_splits() {
@@ -3178,10 +3201,9 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
   a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;
   a.seg_cost = seg_cost_units(a.lds_ring != 0, rows32 ? v32ks : 0);
-  const int pf = rows32 ? v32_ring_depth() : a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
-  // rows32: a ring per key split, then the V scales of key split 0's two row wavefronts (the key-split
-  // merge reuses the rings: 2 x (16 D / 32 + 2) x 64 floats, less than one ring of 3 slots)
-  const size_t lds = rows32     ? (size_t)v32ks * pf * 2 * TILE * head_dim + (size_t)2 * head_dim * sizeof(float)
+  // (verify_kernel has 2-slot rings only with key splits: the instantiated depth sizes the LDS below)
+  const int pf = rows32 ? std::max(v32_ring_depth(), v32ks == 2 ? 2 : 3) : a.lds_ring ? lds_prefetch_depth() : prefetch_depth();
+  const size_t lds = rows32     ? (size_t)v32_lds_bytes(head_dim, pf, v32ks)
                      : a.lds_ring ? (size_t)pf * 2 * TILE * head_dim
                                   : (size_t)(ks - 1) * rt * MERGE_FIELDS * WAVE * sizeof(float);
   void (*kern)(AttnArgs);
@@ -3189,10 +3211,12 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
     auto pick = [&](auto qg_t) -> void (*)(AttnArgs) {
       constexpr int QG = decltype(qg_t)::value;
       if (head_dim == 128) {
-        if (v32ks == 2) return pf == 3 ? verify_kernel<128, 3, QG, 2> : verify_kernel<128, 4, QG, 2>;
+        if (v32ks == 2)
+          return pf == 2 ? verify_kernel<128, 2, QG, 2> : pf == 3 ? verify_kernel<128, 3, QG, 2> : verify_kernel<128, 4, QG, 2>;
         return pf == 3 ? verify_kernel<128, 3, QG, 1> : verify_kernel<128, 4, QG, 1>;
       }
-      if (v32ks == 2) return pf == 3 ? verify_kernel<64, 3, QG, 2> : verify_kernel<64, 4, QG, 2>;
+      if (v32ks == 2)
+        return pf == 2 ? verify_kernel<64, 2, QG, 2> : pf == 3 ? verify_kernel<64, 3, QG, 2> : verify_kernel<64, 4, QG, 2>;
       return pf == 3 ? verify_kernel<64, 3, QG, 1> : verify_kernel<64, 4, QG, 1>;
     };
     kern = q_group == 32 ? pick(std::integral_constant<int, 32>{}) : pick(std::integral_constant<int, 0>{});
