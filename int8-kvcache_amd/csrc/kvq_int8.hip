@@ -58,7 +58,11 @@ constexpr int DEFAULT_SEG_COST = 8;   // a segment's fixed cost, in tile units: 
                                       // lengths; 10 x 32k + 86 x 1 keys) time best at 6-16
 constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kernel (4 row tiles filling
                                                // one ring): verification batches time best at 12
-constexpr int DEFAULT_PREFETCH = 3;
+// register ring of the decode kernel: tiles in flight per wavefront (PF - 1 ahead of the one computed).
+// Under full load HBM latency grows with the bytes in flight (~5 us at 2 tiles ahead per wavefront), and
+// every piece of a segment pays it twice at its start (page ids, then K/V): one tile ahead streams as
+// fast and starts pieces sooner (same-box A/B: c4 decode rows 128.2 -> 124.9 us, c2 645 -> 643 us).
+constexpr int DEFAULT_PREFETCH = 2;
 constexpr int DEFAULT_V32_RING = 2;     // verify_kernel's ring slots (3 with one key split)
 constexpr int DEFAULT_V32_KSPLIT = 2;   // verify_kernel's key splits per workgroup
 constexpr int DEFAULT_SEG_COST_V32_KS2 = 16;  // fixed cost of a segment in verify_kernel with 2 key splits
