@@ -536,7 +536,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / (kern_ms_mean * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(alg / (kern_ms_mean * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_kernel<128,3>", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
+                     "kernel": "attn_kernel<128, 2, false> (one pass)", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
                      "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
     }
     res["c2_other_call"] = {
