@@ -516,6 +516,7 @@ struct AttnArgs {
   int lds_ring;       // 1: the workgroup's wavefronts are row tiles of the same rows (ksplit 1, rt >= 2)
                       // and share each K/V tile through an LDS ring of PF slots (the dynamic LDS)
   int xcd_order;      // map workgroups to workers XCD by XCD
+  long long plan_fast_max;  // the plan's scans run in 32 bits on DPP while every request's units are below this
 };
 
 __device__ __forceinline__ long long uniform64(long long x) {
@@ -585,11 +586,11 @@ __device__ __forceinline__ int wave_incl_max(int x) {
   x = max(x, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
   return x;
 }
-// Inclusive prefix sum of the lanes' v (>= 0): in 32 bits on DPP when every v < 2^24 (64 of them cannot
-// overflow), otherwise by 64-bit shuffles.
+// Inclusive prefix sum of the lanes' v (>= 0): in 32 bits on DPP when every v < fast_max (at most 2^24:
+// 64 of them cannot overflow), otherwise by 64-bit shuffles.
 constexpr long long PLAN_FAST_MAX = 1ll << 24;
-__device__ __forceinline__ long long wave_incl_sum64(long long v, int lane) {
-  if (__ballot(v >= PLAN_FAST_MAX) == 0ull) return (long long)wave_incl_sum((int)v);
+__device__ __forceinline__ long long wave_incl_sum64(long long v, int lane, long long fast_max) {
+  if (__ballot(v >= fast_max) == 0ull) return (long long)wave_incl_sum((int)v);
   long long incl = v;
 #pragma unroll
   for (int o = 1; o < WAVE; o <<= 1) {
@@ -630,7 +631,7 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
     if (c < PLAN_CACHE) {
       u[c] = v; tk[c] = w.tok; ql[c] = w.qlen; ln[c] = w.len;
     }
-    tot += lane_value64(wave_incl_sum64(v, lane), WAVE - 1);
+    tot += lane_value64(wave_incl_sum64(v, lane, a.plan_fast_max), WAVE - 1);
     nmax = max(nmax, __builtin_amdgcn_readlane(wave_incl_max(len), WAVE - 1));
   }
   Plan p;
@@ -657,7 +658,7 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
       w = req_work(a, r);
       v = (long long)seg_units(a, w) * a.hkv * w.rgroups;
     }
-    const long long incl = wave_incl_sum64(v, lane);
+    const long long incl = wave_incl_sum64(v, lane, a.plan_fast_max);
     const long long ctot = lane_value64(incl, WAVE - 1);
     if (base + ctot > pos) {
       const unsigned long long m = __ballot(base + incl > pos);
@@ -3201,6 +3202,9 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.rt = rows32 ? V32_GROUP_TILES : rt; a.ksplit = rows32 ? v32ks : ks; a.waves = waves;
   a.min_tiles = MIN_SPLIT_TILES * a.ksplit;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
+  // KVQ_PLAN_FAST_MAX (tests): a lower bound on units sends the plan's scans down the 64-bit path
+  a.plan_fast_max = getenv("KVQ_PLAN_FAST_MAX") ? std::max(1ll, std::min(PLAN_FAST_MAX, atoll(getenv("KVQ_PLAN_FAST_MAX"))))
+                                                : PLAN_FAST_MAX;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
   a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;

@@ -571,6 +571,36 @@ def test_every_worker_count_covers_the_batch(serving, target_waves, splits):
     check_attention(ref[short], out, "worker_coverage", target_waves=target_waves, splits=splits)
 
 
+@pytest.mark.parametrize("kind", ["decode", "verify"])
+@pytest.mark.parametrize("fast_max", [None, "1"])
+def test_plan_beyond_cached_requests_and_64bit_scans(fast_max, kind):
+    """A batch of 300 requests (more than the plan keeps in registers: the locate scan reloads requests
+    256..299) gives the same result with the plan's 32-bit DPP scans and with its 64-bit shuffle scans
+    (KVQ_PLAN_FAST_MAX=1 forces them) -- the same partition, bit for bit -- and matches the oracle; decode
+    rows run the 16-row kernel, verification rows the 32-row one."""
+    r = synth.rng(23)
+    q_lens = [1] * 280 + ([1] * 20 if kind == "decode" else [int(x) for x in r.integers(2, 9, 20)])
+    seq_lens = [int(x) for x in r.integers(1, 1500, 300)]
+    c = synth.paged_case(28, 4, q_lens, seq_lens, seed=29, params=synth.channel_params(4, 128))
+    c["static"] = synth.calibration_scales(4, 128, synth.channel_params(4, 128))
+    c["scale"] = 128 ** -0.5
+    kq, vq = int8_cache(c)
+    d = dev(c)
+    T = d["q"].shape[0]
+    outs = []
+    for env in (None, fast_max):
+        if env is not None:
+            os.environ["KVQ_PLAN_FAST_MAX"] = env
+        try:
+            outs.append(ck.decode_attention(d["q"], dev(kq), dev(vq), nan_like(d["q"]), d["cu"], d["seq_lens"],
+                                            d["block_table"], c["scale"], d["static"], segm=nan_segm(T, 28, 16, 128),
+                                            max_query_len=max(q_lens)).cpu())
+        finally:
+            os.environ.pop("KVQ_PLAN_FAST_MAX", None)
+    assert torch.equal(outs[0], outs[1])
+    check_attention(oracle_attention(c, kq, vq), outs[1], "plan_300_requests", fast_max=fast_max, kind=kind)
+
+
 # ------------------------------------------------------------------ concurrent streams
 def test_two_streams_merge_independently():
     """Two streams run split attention on different batches at the same time (each with its own split
