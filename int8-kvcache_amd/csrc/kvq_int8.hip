@@ -1427,12 +1427,14 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
 constexpr int V32_GROUP_TILES = 4;
 // verify_kernel's dynamic LDS: KS rings of PF slots (K then V rows of 32 keys), which the key-split
 // merge reuses (2 row wavefronts x (16 D / 32 + 2) fields x 64 lanes of fp32) -- at least as large as
-// either -- then the V scales of key split 0's two row wavefronts
+// either -- then the V scales of key split 0's two row wavefronts, then every wavefront's K scales
 constexpr int64_t v32_vscale_offset(int64_t d, int64_t pf, int64_t ks) {
   const int64_t rings = ks * pf * 2 * TILE * d, merge = ks == 2 ? 2 * (16 * (d / 32) + 2) * WAVE * 4 : 0;
   return rings > merge ? rings : merge;
 }
-constexpr int64_t v32_lds_bytes(int64_t d, int64_t pf, int64_t ks) { return v32_vscale_offset(d, pf, ks) + 2 * d * 4; }  // 16-row tiles per row group (the stream-K plan's unit of rows)
+constexpr int64_t v32_lds_bytes(int64_t d, int64_t pf, int64_t ks) {
+  return v32_vscale_offset(d, pf, ks) + (2 + 2 * ks) * d * 4;   // V scales of 2 wavefronts, K scales of all
+}  // 16-row tiles per row group (the stream-K plan's unit of rows)
 
 template <int CHR>
 __device__ __forceinline__ int swz_k(int row) { return (row >> 1) & (CHR - 1); }
@@ -1445,7 +1447,8 @@ __device__ __forceinline__ int swz_v(int row) { return ((((row >> 1) & 1) | (((r
 template <int D, int PF, int QG, int KS>
 __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int tok, int qlen, int seqlen, int kvh, int row0,
                                               int c_begin, int c_end, int wave, int kw, bool active, int part,
-                                              int nparts, uint8_t* ring, float* vsl, float* merge, int lane) {
+                                              int nparts, uint8_t* ring, float* vsl, float* ksl, float* merge,
+                                              int lane) {
   constexpr int KST = D / 32;       // 32-channel QK steps = 32-channel PV tiles
   constexpr int CHR = D / 16;       // 16-byte chunks per K (or V) row
   constexpr int RPI = WAVE / CHR;   // rows per DMA instruction
@@ -1554,7 +1557,6 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
   {
     const bool qrow = rtok < qlen && active;
     u32x4 qw[2 * KST];
-    float4 kf[4 * KST];
     if (qrow) {
       const uint16_t* qp = a.q + (int64_t)(tok + rtok) * a.q_st + (int64_t)(kvh * G + rh) * a.q_sh + 16 * h;
 #pragma unroll
@@ -1562,14 +1564,11 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
         qw[2 * s] = *reinterpret_cast<const u32x4*>(qp + 32 * s);
         qw[2 * s + 1] = *reinterpret_cast<const u32x4*>(qp + 32 * s + 8);
       }
-      if (a.ks_pc) {
-        const float* kp = a.ks + kvh * D + 16 * h;
-#pragma unroll
-        for (int s = 0; s < KST; ++s)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) kf[4 * s + u] = *reinterpret_cast<const float4*>(kp + 32 * s + 4 * u);
-      }
     }
+    // the K scales go through this wavefront's LDS slice too: 2 per lane here, 16 per lane read back
+    // below (in registers they would hold 16 D / 32 VGPRs through the prologue)
+    float2 ks2 = {0.f, 0.f};
+    if (a.ks_pc && 2 * lane < D) ks2 = *reinterpret_cast<const float2*>(a.ks + kvh * D + 2 * lane);
     float2 vs2 = {0.f, 0.f};
     if (kw == 0 && a.vs_pc && 2 * lane < D) vs2 = *reinterpret_cast<const float2*>(a.vs + kvh * D + 2 * lane);
     if (nt > 0) {
@@ -1581,6 +1580,7 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
       for (int j = 0; j < PF - 1; ++j) dma_page(min(tile_of(j), c_end - 1), j, pg[j]);
     }
     if (kw == 0 && a.vs_pc && 2 * lane < D) *reinterpret_cast<float2*>(vsl + 2 * lane) = vs2;
+    if (a.ks_pc && 2 * lane < D) *reinterpret_cast<float2*>(ksl + 2 * lane) = ks2;
     float x[16 * KST];
     float amax = 0.f;
     if (qrow) {
@@ -1599,7 +1599,7 @@ __device__ __forceinline__ void attend_rows32(const AttnArgs& a, int seq, int to
         for (int s = 0; s < KST; ++s)
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
-            const float4 f = kf[4 * s + u];
+            const float4 f = *reinterpret_cast<const float4*>(ksl + 32 * s + 16 * h + 4 * u);
             x[16 * s + 4 * u] *= f.x; x[16 * s + 4 * u + 1] *= f.y;
             x[16 * s + 4 * u + 2] *= f.z; x[16 * s + 4 * u + 3] *= f.w;
           }
@@ -1926,6 +1926,7 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
   uint8_t* rings = reinterpret_cast<uint8_t*>(v32_lds);
   uint8_t* ring = rings + kw * PF * SLOT;
   float* vsl = reinterpret_cast<float*>(rings + v32_vscale_offset(D, PF, KS)) + rw * D;
+  float* ksl = reinterpret_cast<float*>(rings + v32_vscale_offset(D, PF, KS)) + (2 + wave) * D;
   float* merge = reinterpret_cast<float*>(rings);
   int worker = blockIdx.x;
   if (a.xcd_order) {
@@ -1956,7 +1957,7 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
     const int c1 = whole ? (off == 0 ? w.ntiles : 0) : max(off + take - fc, 0);
     if (c1 > c0)
       attend_rows32<D, PF, QG, KS>(a, r, w.tok, w.qlen, w.len, kvh, row0, c0, c1, rw, kw, row0 < w.qlen * a.G,
-                                   (int)(worker - first), (int)(last - first + 1), ring, vsl, merge, lane);
+                                   (int)(worker - first), (int)(last - first + 1), ring, vsl, ksl, merge, lane);
     pos += take;
     off = 0;
     if (++seg == a.hkv * w.rgroups && pos < end) {  // on to the next request with work
