@@ -564,6 +564,12 @@ __device__ __forceinline__ int seg_units(const AttnArgs& a, const ReqWork& w) {
 struct Plan {
   long long total, chunk;
 };
+// a / b for 0 <= a, 0 < b: 32-bit division when both fit (every practical batch; a 64-bit division is a
+// long instruction sequence, and the plan and each piece need a few)
+__device__ __forceinline__ long long udiv_plan(long long a, long long b) {
+  if (((unsigned long long)a | (unsigned long long)b) >> 32 == 0ull) return (long long)((unsigned)a / (unsigned)b);
+  return a / b;
+}
 
 // Inclusive prefix sum / maximum of x over the wavefront's 64 lanes on DPP: row shifts by 1, 2, 4, 8
 // within each 16-lane row, then lane 15's value added into rows 1 and 3 and lane 31's into rows 2
@@ -636,7 +642,7 @@ __device__ Plan plan_and_locate(const AttnArgs& a, int worker, int lane, int& r_
   }
   Plan p;
   p.total = tot;
-  long long ch = (p.total + a.workers - 1) / a.workers;
+  long long ch = udiv_plan(p.total + a.workers - 1, a.workers);
   if (nmax > 0) {
     ch = max(ch, (long long)((nmax + a.max_splits - 2) / (a.max_splits - 1)));
     ch = max(ch, (long long)a.min_tiles);
@@ -1352,7 +1358,7 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   const long long end = min(pos + pl.chunk, pl.total);
   if (pos >= end || r >= a.num_seqs) return;
   int seglen = seg_units(a, w);
-  int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
+  int seg = (int)udiv_plan(pos - rstart, seglen), off = (int)(pos - rstart - (long long)seg * seglen);
   bool whole = !cuttable(a, w);
   int solo = 0;  // pieces run by a single wavefront so far (uniform across the workgroup)
   while (pos < end) {
@@ -1363,8 +1369,8 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
     // the pieces are numbered from the worker holding the first tile). Uncut (whole): the worker where
     // the segment starts runs all of it, one piece.
     const int fc = a.seg_cost;
-    const long long first = whole ? worker : (seg_start + fc) / pl.chunk;
-    const long long last = whole ? worker : (seg_start + seglen - 1) / pl.chunk;
+    const long long first = whole ? worker : udiv_plan(seg_start + fc, pl.chunk);
+    const long long last = whole ? worker : udiv_plan(seg_start + seglen - 1, pl.chunk);
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
     const int row0 = (rg * a.rt + rtile) * 16;
     const int c0 = whole ? 0 : max(off - fc, 0);
@@ -1943,14 +1949,14 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
   const long long end = min(pos + pl.chunk, pl.total);
   if (pos >= end || r >= a.num_seqs) return;
   int seglen = seg_units(a, w);
-  int seg = (int)((pos - rstart) / seglen), off = (int)((pos - rstart) % seglen);
+  int seg = (int)udiv_plan(pos - rstart, seglen), off = (int)(pos - rstart - (long long)seg * seglen);
   bool whole = !cuttable(a, w);
   while (pos < end) {
     const long long seg_start = rstart + (long long)seg * seglen;
     const int take = (int)min((long long)(seglen - off), end - pos);
     const int fc = a.seg_cost;
-    const long long first = whole ? worker : (seg_start + fc) / pl.chunk;
-    const long long last = whole ? worker : (seg_start + seglen - 1) / pl.chunk;
+    const long long first = whole ? worker : udiv_plan(seg_start + fc, pl.chunk);
+    const long long last = whole ? worker : udiv_plan(seg_start + seglen - 1, pl.chunk);
     const int kvh = seg / w.rgroups, rg = seg % w.rgroups;
     const int row0 = rg * (16 * V32_GROUP_TILES) + 32 * rw;
     const int c0 = whole ? 0 : max(off - fc, 0);
