@@ -92,17 +92,7 @@ __device__ __forceinline__ uint32_t pack_i8x4(float a, float b, float c, float d
 }
 
 // Code of x / s: rint of the correctly rounded fp32 quotient, saturated to [-127, 127]
-// (kvq/quant.py:50-51). r = fl(1 / s) (IEEE division, once per channel), so q0 = fl(x * r) is within
-// |q0| * 1.6 * 2^-23 of fl(x / s); when q0 is farther than |q0| * 2^-21 from every half-integer,
-// rint(q0) equals rint(fl(x / s)). `bad` is set for the rare element that needs the exact division
-// instead. |q0| >= 128 saturates either way.
-__device__ __forceinline__ float code_fast(float x, float r, bool& bad) {
-  const float q0 = x * r;
-  const float n = __builtin_rintf(q0);
-  const float aq = __builtin_fabsf(q0);
-  bad |= (__builtin_fabsf(q0 - n) >= __builtin_fmaf(aq, -0x1p-21f, 0.5f)) & (aq < 128.f);
-  return sat127(n);
-}
+// (kvq/quant.py:50-51), by IEEE division.
 __device__ __forceinline__ float code_exact(float x, float s) { return sat127(__builtin_rintf(x / s)); }
 
 // x / 127, correctly rounded, for every float x in [2^-126, 1] (the range of a P tile maximum):
@@ -150,7 +140,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // ------------------------------------------------------------------------------------------------
 // Fused quantize + reshape_and_cache (reference kvq/cuda/int8_kv.cu:55-84).
-// Each lane owns 8 channels of one head for the whole launch (their reciprocal scales and K means in
+// Each lane owns 8 channels of one head for the whole launch (their scales' reciprocals and K means in
 // registers), so a token's K and V rows are read as contiguous runs (1 KB each for H = 4, D = 128) and
 // each (token, head) writes its 128-byte K and V code rows with 16 consecutive lanes -- the 256-byte
 // K|V run of a slot in vLLM's interleaved layout. Two kernels: quant_cache_rows_kernel when a token's
@@ -158,15 +148,11 @@ __device__ __forceinline__ float wave_sum(float x) {
 // (lanes of a wavefront may hold different tokens). Both walk their tokens with a ring of loads in
 // flight.
 //
-// Codes: with r = v_rcp_f32(s) (within 1 ulp of 1/s) and M = 1.5 * 2^23, t = fma(x, r, M) rounds
-// the exact product x * r once: t - M = rint(x * r) (ties to even) while |x * r| < 2^22, held in t's
-// low mantissa bits, so the code byte is read straight out of clamp(t, M +- 127). The exact x * r is
-// within 1.5 * 2^-23 * |x / s| (<= 2.3e-5 for |x / s| <= 127.5) of fl(x / s); e = fma(x, r, -(t - M))
-// = x * r - rint(x * r) (one rounding, 2^-25) tells how close it is to a rounding boundary. Lanes
-// with |e| >= 0.5 - 2^-14 (6.1e-5) redo their 8 channels with IEEE division; below it
-// rint(fl(x / s)) = rint(x * r), and clamping commutes with rint. |x * r| >= 2^22 means |x / s| >
-// 127.5: either e flags it or t clamps to +-127, the saturated code. Checked on the host over 6.7e9
-// (x, s, r) cases (tests/arith/quant_round_check.c).
+// Codes: code_magic per channel -- the correctly rounded quotient fl(x / s) from the lane's y = fl(1 / s)
+// and the scale itself in three operations, rounded to an integer by adding M = 1.5 * 2^23 (ties to
+// even), which leaves the code in t's low mantissa bits, so the code byte is read straight out of
+// clamp(t, M +- 127). No branch: ties (x / s exactly k + 0.5 -- common with bf16 inputs, e.g. x at
+// half a channel's absolute maximum) cost nothing extra.
 // ------------------------------------------------------------------------------------------------
 constexpr int QC_CPL = 8;     // channels per lane
 #ifndef QC_PF
@@ -194,6 +180,20 @@ __device__ __forceinline__ void qc_store(T v, T* p) {
   else *p = v;
 }
 
+// The same code as code_exact, plus QC_MAGIC, without a division: y = fl(1 / s) (IEEE division, once
+// per channel), so q = fl(x * y) is within an ulp of x / s, the remainder x - q s is exact in one FMA
+// and q + (x - q s) y, rounded once, is fl(x / s) (Markstein's theorem: a correctly rounded quotient
+// from a correctly rounded reciprocal); adding QC_MAGIC (1.5 * 2^23, even) then rounds that to an
+// integer, ties to even, as rint does. q is first clamped to +-254: a quotient beyond it, infinite
+// included, then still comes out beyond +-127 (instead of a NaN remainder) and saturates. Checked
+// against code_exact on the host for every finite and infinite bf16 x and fp32 x on and next to the
+// ties, over thousands of scales (tests/test_arith.py).
+__device__ __forceinline__ float code_magic(float x, float s, float y) {
+  const float q = __builtin_fminf(__builtin_fmaxf(x * y, -254.f), 254.f);
+  const float qf = __builtin_fmaf(__builtin_fmaf(-q, s, x), y, q);
+  return __builtin_fminf(__builtin_fmaxf(qf + QC_MAGIC, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
+}
+
 // code bytes (little endian) of 4 values t = fl(c + QC_MAGIC)
 __device__ __forceinline__ uint32_t pack_magic4(float t0, float t1, float t2, float t3) {
   const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(t1), __float_as_uint(t0), 0x0c0c0400u);
@@ -214,10 +214,10 @@ __device__ __forceinline__ void load_scales8(const float* __restrict__ p, int pc
   }
 }
 
-// r: reciprocals of the lane's 8 scales; get_sc(sc) fetches the scales themselves, for the rare exact
-// pass only (so that they hold no registers)
+// y: fl(1 / s) of the lane's 8 scales s; get_sc(sc) fetches the scales themselves (at the call, so that
+// they hold no registers between tokens)
 template <bool SUB_MU, typename GetScales>
-__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], GetScales get_sc, const float (&mu)[QC_CPL]) {
+__device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&y)[QC_CPL], GetScales get_sc, const float (&mu)[QC_CPL]) {
   float x[QC_CPL], t[QC_CPL];
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -229,20 +229,10 @@ __device__ __forceinline__ u32x2 quant8(u32x4 w, const float (&r)[QC_CPL], GetSc
 #pragma unroll
     for (int e = 0; e < QC_CPL; ++e) x[e] = x[e] - mu[e];
   }
-  float worst = 0.f;
+  float sc[QC_CPL];
+  get_sc(sc);
 #pragma unroll
-  for (int e = 0; e < QC_CPL; ++e) {
-    const float t0 = __builtin_fmaf(x[e], r[e], QC_MAGIC);            // rint(x r) + M, one rounding
-    const float res = __builtin_fmaf(x[e], r[e], -(t0 - QC_MAGIC));   // x r - rint(x r)
-    worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
-    t[e] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
-  }
-  if (worst >= 0.5f - 0x1p-14f) {  // rare: a quotient near a half-integer -- redo this lane exactly
-    float sc[QC_CPL];
-    get_sc(sc);
-#pragma unroll
-    for (int e = 0; e < QC_CPL; ++e) t[e] = code_exact(x[e], sc[e]) + QC_MAGIC;
-  }
+  for (int e = 0; e < QC_CPL; ++e) t[e] = code_magic(x[e], sc[e], y[e]);
   return u32x2{pack_magic4(t[0], t[1], t[2], t[3]), pack_magic4(t[4], t[5], t[6], t[7])};
 }
 
@@ -296,8 +286,8 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAV
       if (j < steps) fetch(j, j);
 #pragma unroll
     for (int e = 0; e < QC_CPL; ++e) {
-      kr[e] = __builtin_amdgcn_rcpf(kr[e]);
-      vr[e] = __builtin_amdgcn_rcpf(vr[e]);
+      kr[e] = 1.f / kr[e];
+      vr[e] = 1.f / vr[e];
     }
 #pragma unroll
     for (int j = 0; j < QC_PF - 1; ++j)
@@ -308,8 +298,8 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAV
   for (int j = 0; j < QC_PF - 1; ++j) fetch(j, j);
 #pragma unroll
   for (int e = 0; e < QC_CPL; ++e) {
-    kr[e] = __builtin_amdgcn_rcpf(kr[e]);
-    vr[e] = __builtin_amdgcn_rcpf(vr[e]);
+    kr[e] = 1.f / kr[e];
+    vr[e] = 1.f / vr[e];
   }
   for (int k0 = 0; k0 < steps; k0 += QC_PF) {
 #pragma unroll
@@ -333,7 +323,7 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAV
 // as precise as the compiler's static count of what was issued: so nothing here issues a vector
 // memory operation under a branch. A padded slot (or a ring entry past the wavefront's last token)
 // still stores, through a descriptor with no records, which the hardware's range check drops; the
-// exact pass reads its scales from LDS. The ring's waits then leave QC_ROW_PF - 1 tokens' loads and
+// scales come from LDS at each token. The ring's waits then leave QC_ROW_PF - 1 tokens' loads and
 // the stores of earlier tokens in flight instead of draining them per token.
 #ifndef QC_ROW_PF
 #define QC_ROW_PF 4           // ring of token loads per wavefront (QC_ROW_PF - 1 in flight ahead)
@@ -428,8 +418,8 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
     tab8(2, mu);
 #pragma unroll
     for (int e = 0; e < QC_CPL; ++e) {
-      kr[e] = __builtin_amdgcn_rcpf(kr[e]);
-      vr[e] = __builtin_amdgcn_rcpf(vr[e]);
+      kr[e] = 1.f / kr[e];
+      vr[e] = 1.f / vr[e];
     }
   };
   if (steps <= QC_ROW_PF - 1) {
@@ -704,32 +694,16 @@ __device__ __forceinline__ void wait_vm() {
 // flight (they write LDS), which the rings keep outstanding on purpose.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// code bytes of q: rint(x / s) saturated, from r = rcp(s) with the rounding shortcut of quant8 (exact
-// division for a lane whose quotients come near a half-integer); x holds the lane's N channels. Codes
-// are packed as they are made, so only x and the packed words are live at once.
+// code bytes of q: rint(x / s) saturated (code_magic, one IEEE division for the row's scale); x holds
+// the lane's N channels. Codes are packed as they are made, so only x and the packed words are live at
+// once.
 template <int N>
 __device__ __forceinline__ void q_codes(const float (&x)[N], float s, uint32_t (&out)[N / 4]) {
-  const float r = __builtin_amdgcn_rcpf(s);
-  float worst = 0.f;
+  const float y = 1.f / s;
 #pragma unroll
-  for (int u = 0; u < N / 4; ++u) {
-    float t[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float xe = x[4 * u + i];
-      const float t0 = __builtin_fmaf(xe, r, QC_MAGIC);
-      const float res = __builtin_fmaf(xe, r, -(t0 - QC_MAGIC));
-      worst = __builtin_fmaxf(worst, __builtin_fabsf(res));
-      t[i] = __builtin_fminf(__builtin_fmaxf(t0, QC_MAGIC - 127.f), QC_MAGIC + 127.f);
-    }
-    out[u] = pack_magic4(t[0], t[1], t[2], t[3]);
-  }
-  if (worst >= 0.5f - 0x1p-14f) {
-#pragma unroll
-    for (int u = 0; u < N / 4; ++u)
-      out[u] = pack_magic4(code_exact(x[4 * u], s) + QC_MAGIC, code_exact(x[4 * u + 1], s) + QC_MAGIC,
-                           code_exact(x[4 * u + 2], s) + QC_MAGIC, code_exact(x[4 * u + 3], s) + QC_MAGIC);
-  }
+  for (int u = 0; u < N / 4; ++u)
+    out[u] = pack_magic4(code_magic(x[4 * u], s, y), code_magic(x[4 * u + 1], s, y), code_magic(x[4 * u + 2], s, y),
+                         code_magic(x[4 * u + 3], s, y));
 }
 
 template <int D>

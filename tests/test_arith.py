@@ -24,10 +24,11 @@ def test_div127_is_ieee_division_on_all_tile_maxima(tmp_path):
     assert rc == 0 and out.endswith("mismatched 0"), out
 
 
-def test_quant_cache_rounding_shortcut_matches_ieee_codes(tmp_path):
-    """quant_cache's codes: t = fma(x, r, 1.5 * 2^23), e = fma(x, r, -(t - 1.5 * 2^23)) with r within
-    1 ulp of 1/s give clamp(rint(fl(x / s)), +-127) whenever |e| < 0.5 - 2^-14 (the kernel's exact
-    pass covers the rest): every finite bf16 and 2^20 random fp32 x, 2000 scales (a quarter of them
-    putting some x exactly on a tie), r at RN(1/s) and one ulp either side."""
-    rc, out = _run_c(tmp_path, "quant_round_check")
+def test_division_free_codes_match_ieee_codes(tmp_path):
+    """The cache write's and the q quantization's codes (code_magic): q = clamp(fl(x * y), +-254) with
+    y = fl(1 / s), f = fma(fma(-q, s, x), y, q), t = clamp(fl(f + 1.5 * 2^23), +-127) give
+    clamp(rint(fl(x / s)), +-127) bit for bit: every bf16 but NaN (infinities included), 2^20 random
+    fp32 x and fp32 x on and within 4 ulps of half-integer quotients, 2400 scales (a third of them
+    bf16 absolute maxima / 127, a third putting a chosen x exactly on a tie)."""
+    rc, out = _run_c(tmp_path, "quant_exact_check")
     assert rc == 0 and out.endswith("mismatched 0"), out
