@@ -354,9 +354,10 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
   const int stride = (gridDim.x / wpt) * WPB;
   const int h = part * HPW + lane / LPH, d0 = (lane % LPH) * QC_CPL;
 
-  // the part's scales and k_mu, loaded once per workgroup: every wavefront of the grid reads the
-  // same few lines of these tables, so per-wavefront loads would pile onto a few L2 channels
-  __shared__ float4 tab[3][CH / 4];               // k_scale, v_scale, k_mu of channels part * CH + c
+  // the part's scales, k_mu and the scales' reciprocals (IEEE division), made once per workgroup: every
+  // wavefront of the grid reads the same few lines of these tables, so per-wavefront loads would pile
+  // onto a few L2 channels, and a wavefront's own divisions would cost as much as its tokens' codes
+  __shared__ float4 tab[5][CH / 4];  // k_scale, v_scale, k_mu, 1 / k_scale, 1 / v_scale of channels part * CH + c
   for (int i = threadIdx.x; i < 3 * CH / 4; i += QC_BLOCK) {
     const int t = i / (CH / 4), c = (i % (CH / 4)) * 4, ch = part * CH + c;
     float4 v;
@@ -365,6 +366,7 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
       const float* tb = t == 0 ? ks : vs;
       if (t == 0 ? ks_pc : vs_pc) v = *reinterpret_cast<const float4*>(tb + ch);
       else { const float x = tb[ch / D]; v = float4{x, x, x, x}; }   // 4 channels never straddle a head
+      tab[3 + t][i % (CH / 4)] = float4{1.f / v.x, 1.f / v.y, 1.f / v.z, 1.f / v.w};
     }
     tab[t][i % (CH / 4)] = v;
   }
@@ -413,14 +415,9 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
                                           wv, vcoff, 0, QC_STORE_AUX);
   };
   auto prepare = [&] {
-    tab8(0, kr);
-    tab8(1, vr);
+    tab8(3, kr);
+    tab8(4, vr);
     tab8(2, mu);
-#pragma unroll
-    for (int e = 0; e < QC_CPL; ++e) {
-      kr[e] = 1.f / kr[e];
-      vr[e] = 1.f / vr[e];
-    }
   };
   if (steps <= QC_ROW_PF - 1) {
     // all of the wavefront's tokens in flight at once (entries past the last re-read it, and drop
