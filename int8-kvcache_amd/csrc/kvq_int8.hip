@@ -476,6 +476,19 @@ __global__ __launch_bounds__(256) void quant_q_kernel(const uint16_t* __restrict
 // INT8 attention for short queries.
 // ------------------------------------------------------------------------------------------------
 struct AttnArgs {
+  // What every workgroup reads first (the worker order and the plan), in the first 64 bytes of the
+  // kernel arguments: one scalar-cache line, one memory round trip at launch.
+  const int* cu_q;
+  const int* seq_lens;
+  int num_seqs, hkv, G, qmax;
+  int max_splits;     // split buffers hold this many pieces per (token, q head); 1 = no split buffers
+  int cut_rows;       // the split buffers' rows: tokens [0, cut_rows); a request with a token beyond is never cut
+  int rt;             // row tiles per workgroup: consecutive 16-row tiles of one (request, kv head)
+  int workers;        // workgroups of the attention grid
+  int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
+  int seg_cost;       // work units a segment costs beyond its tiles (its fixed start and finish)
+  int xcd_order;      // map workgroups to workers XCD by XCD
+  int plan_fast_max;  // the plan's scans run in 32 bits on DPP while every request's units are below this
   const uint16_t* q;
   const int8_t* kc;
   const int8_t* vc;
@@ -483,28 +496,18 @@ struct AttnArgs {
   float* segm_out;
   float* segm_max;
   float* segm_sum;
-  const int* cu_q;
-  const int* seq_lens;
   const int* block_table;
   const float* ks;
   const float* vs;
   int64_t q_st, q_sh, o_st, o_sh, k_sb, k_sn, k_sh, v_sb, v_sn, v_sh, seg_st, seg_sh, bt_stride;
   float sm_log2;      // softmax_scale * log2(e)
-  int num_blocks, lbs, G, qmax, ks_pc, vs_pc;
-  int num_seqs, hkv;
-  int max_splits;     // split buffers hold this many pieces per (token, q head); 1 = no split buffers
-  int cut_rows;       // the split buffers' rows: tokens [0, cut_rows); a request with a token beyond is never cut
-  int rt;             // row tiles per workgroup: consecutive 16-row tiles of one (request, kv head)
+  int num_blocks, lbs, ks_pc, vs_pc;
   int ksplit;         // key splits per workgroup: wavefront (t, k) takes every ksplit-th key tile of row tile t
   int waves;          // rt * ksplit wavefronts per workgroup
-  int workers;        // workgroups of the attention grid
-  int min_tiles;      // shortest piece of a cut segment, in 32-key tiles
-  int seg_cost;       // work units a segment costs beyond its tiles (its fixed start and finish)
   int lds_ring;       // 1: the workgroup's wavefronts are row tiles of the same rows (ksplit 1, rt >= 2)
                       // and share each K/V tile through an LDS ring of PF slots (the dynamic LDS)
-  int xcd_order;      // map workgroups to workers XCD by XCD
-  long long plan_fast_max;  // the plan's scans run in 32 bits on DPP while every request's units are below this
 };
+static_assert(offsetof(AttnArgs, q) == 64, "the plan's arguments fill the first 64 bytes");
 
 __device__ __forceinline__ long long uniform64(long long x) {
   const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)(x & 0xffffffffll));
@@ -1315,12 +1318,12 @@ __global__ __launch_bounds__(256) void attn_kernel(AttnArgs a) {
   // XCD x holds the blocks b = x (mod 8), q + (x < rem) of them for W = 8 q + rem, and takes the
   // workers [x q + min(x, rem), ...) -- consecutive ranges that tile [0, W) exactly.
   int worker = blockIdx.x;
-  if (a.xcd_order) {
+  {  // no branch before the plan: its argument loads go out in one batch
     const int q = a.workers / NUM_XCDS, rem = a.workers % NUM_XCDS;
     const int wx = blockIdx.x % NUM_XCDS, wi = blockIdx.x / NUM_XCDS;
-    worker = wx * q + min(wx, rem) + wi;
+    worker = a.xcd_order ? wx * q + min(wx, rem) + wi : worker;
+    worker = (int)blockIdx.x < a.workers ? worker : a.workers;   // past the grid's workers: no units
   }
-  if (worker >= a.workers) return;
   int r;
   long long rstart;
   ReqWork w;
@@ -1906,12 +1909,12 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
   float* ksl = reinterpret_cast<float*>(rings + v32_vscale_offset(D, PF, KS)) + (2 + wave) * D;
   float* merge = reinterpret_cast<float*>(rings);
   int worker = blockIdx.x;
-  if (a.xcd_order) {
+  {  // no branch before the plan: its argument loads go out in one batch
     const int q = a.workers / NUM_XCDS, rem = a.workers % NUM_XCDS;
     const int wx = blockIdx.x % NUM_XCDS, wi = blockIdx.x / NUM_XCDS;
-    worker = wx * q + min(wx, rem) + wi;
+    worker = a.xcd_order ? wx * q + min(wx, rem) + wi : worker;
+    worker = (int)blockIdx.x < a.workers ? worker : a.workers;   // past the grid's workers: no units
   }
-  if (worker >= a.workers) return;
   int r;
   long long rstart;
   ReqWork w;
@@ -3181,8 +3184,8 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   a.min_tiles = MIN_SPLIT_TILES * a.ksplit;
   a.xcd_order = getenv("KVQ_XCD_ORDER") ? atoi(getenv("KVQ_XCD_ORDER")) : 1;
   // KVQ_PLAN_FAST_MAX (tests): a lower bound on units sends the plan's scans down the 64-bit path
-  a.plan_fast_max = getenv("KVQ_PLAN_FAST_MAX") ? std::max(1ll, std::min(PLAN_FAST_MAX, atoll(getenv("KVQ_PLAN_FAST_MAX"))))
-                                                : PLAN_FAST_MAX;
+  a.plan_fast_max = getenv("KVQ_PLAN_FAST_MAX") ? (int)std::max(1ll, std::min(PLAN_FAST_MAX, atoll(getenv("KVQ_PLAN_FAST_MAX"))))
+                                                : (int)PLAN_FAST_MAX;
   // row tiles of the same rows without key splits share each K/V tile through an LDS ring
   // (KVQ_LDS_RING=0: off), of lds_prefetch_depth() slots
   a.lds_ring = (rows32 || (ks == 1 && rt >= 2 && !(getenv("KVQ_LDS_RING") && atoi(getenv("KVQ_LDS_RING")) == 0))) ? 1 : 0;
