@@ -44,16 +44,27 @@ DEV = "cuda"
 
 # ------------------------------------------------------------------------------------------------ HIP events
 class HipEvents:
-    """Raw hipEvent_t pairs (the library records them on the stream it launches on)."""
+    """Raw hipEvent_t pairs, for timing only: created without the system-scope fence at record
+    (hipEventDisableSystemFence), whose cache writeback and invalidation cost ~2.5 us per recorded
+    event on these boxes. The library records pairs around its next attention kernel
+    (kvq_set_attention_events); record() puts one on a given stream."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
 
     def __init__(self, n):
         self.hip = ctypes.CDLL("libamdhip64.so")
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.pairs = []
         for _ in range(n):
             a, b = ctypes.c_void_p(), ctypes.c_void_p()
-            assert self.hip.hipEventCreate(ctypes.byref(a)) == 0 and self.hip.hipEventCreate(ctypes.byref(b)) == 0
+            assert self.hip.hipEventCreateWithFlags(ctypes.byref(a), self.DISABLE_SYSTEM_FENCE) == 0
+            assert self.hip.hipEventCreateWithFlags(ctypes.byref(b), self.DISABLE_SYSTEM_FENCE) == 0
             self.pairs.append((a, b))
+
+    def record(self, i, which, stream):
+        assert self.hip.hipEventRecord(self.pairs[i][which], ctypes.c_void_p(stream)) == 0
 
     def elapsed_ms(self, i):
         ms = ctypes.c_float()
@@ -102,7 +113,14 @@ def backend_passes_split_buffers(q_lens, seq_lens, num_kv_heads):
 def time_c2(w, steps, warmup, split=True):
     """Step time and attention-kernel time of c2. split: the call carries split buffers allocated once
     beforehand, as the vLLM backend's (SPLIT_PIECES pieces per row); otherwise the one-pass call without
-    them (nothing cut, nothing allocated)."""
+    them (nothing cut, nothing allocated).
+
+    The timed region (host clock between two device synchronizations) holds exactly the steps' calls,
+    bracketed by one pair of HIP events on the launch stream: their interval / steps is the average
+    launch duration of the call's kernels (the one-pass call is one kernel; gaps between launches
+    included). Per-kernel durations -- the library's event pair around each attention kernel -- come
+    from as many calls again right after, outside the timed region (a recorded event costs ~2.5 us of
+    the step even without the system fence)."""
     out = torch.empty_like(w["q"])
     scale = w["d"] ** -0.5
     splits = ck.SPLIT_PIECES if split else 1
@@ -113,19 +131,28 @@ def time_c2(w, steps, warmup, split=True):
 
     for _ in range(warmup):
         step()
-    ev = HipEvents(steps)
-    lib = _native.load()
+    region = HipEvents(1)
+    stream = torch.cuda.current_stream().cuda_stream
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    region.record(0, 0, stream)
+    for i in range(steps):
+        step()
+    region.record(0, 1, stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    region_ms = region.elapsed_ms(0) / steps
+    region.close()
+    ev = HipEvents(steps)
+    lib = _native.load()
     for i in range(steps):
         a, b = ev.pairs[i]
         lib.kvq_set_attention_events(a, b)
         step()
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
     kern_ms = [ev.elapsed_ms(i) for i in range(steps)]
     ev.close()
-    return out, (t1 - t0) * 1e3 / steps, statistics.mean(kern_ms), statistics.median(kern_ms), splits
+    return out, (t1 - t0) * 1e3 / steps, region_ms, statistics.mean(kern_ms), statistics.median(kern_ms), splits
 
 
 def read_ceiling(buf, reps=10):
@@ -512,8 +539,8 @@ def main():
     # the other call is timed first, after 30 untimed calls (~20 ms): a GPU that has idled while the host
     # built the workload runs the first ~20 ms of calls ~3% slower (measured: 668 vs 645 us per kernel,
     # both variants, whichever runs first), so both timings start from a busy GPU
-    _, ms1, k1_mean, _, s1 = time_c2(w, max(5, args.steps // 2), 30, split=not split)
-    out, ms_step, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup, split=split)
+    _, ms1, _, k1_mean, _, s1 = time_c2(w, max(5, args.steps // 2), 30, split=not split)
+    out, ms_step, launch_ms, kern_ms_mean, kern_ms_med, splits = time_c2(w, args.steps, args.warmup, split=split)
     alg = w["alg_bytes"]
     res = {
         "metric": METRIC,
@@ -534,10 +561,15 @@ def main():
                            "pass, nothing allocated)" if not split else
                            "kvq.cuda_kernels.decode_attention with split buffers, as the vLLM backend calls it",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": round(alg / (kern_ms_mean * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
-                     "unit": "GB/s", "frac": round(alg / (kern_ms_mean * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
-                     "kernel": "attn_kernel<128, 2, false> (one pass)", "kernel_us_mean": round(kern_ms_mean * 1e3, 1),
-                     "kernel_us_median": round(kern_ms_med * 1e3, 1), "alg_bytes_per_launch": alg},
+        "roofline": {"bound": "hbm", "achieved": round(alg / (launch_ms * 1e-3) / 1e9, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(alg / (launch_ms * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None,
+                     "kernel": "attn_kernel<128, 2, false> (one pass)",
+                     "launch_us_timed_region": round(launch_ms * 1e3, 1),
+                     "how": "algorithmic bytes / (HIP event interval around the timed region's launches / steps)",
+                     "kernel_us_mean": round(kern_ms_mean * 1e3, 1), "kernel_us_median": round(kern_ms_med * 1e3, 1),
+                     "kernel_events": "the library's event pair around each attention kernel, as many calls again "
+                                      "right after the timed region",
+                     "alg_bytes_per_launch": alg},
     }
     res["c2_other_call"] = {
         "what": ("with split buffers allocated once beforehand (%d pieces per row at most, the vLLM backend's "
