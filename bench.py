@@ -167,14 +167,14 @@ def read_ceiling(buf, reps=10):
         out = torch.empty(wg * 256, dtype=torch.int32, device=DEV)
         for _ in range(2):
             _native.call("kvq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), wg, stream)
-        ts = []
-        for _ in range(reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
+        ev = HipEvents(reps)
+        for i in range(reps):
+            ev.record(i, 0, stream)
             _native.call("kvq_stream_read", buf.data_ptr(), nbytes, out.data_ptr(), wg, stream)
-            b.record()
-            b.synchronize()
-            ts.append(a.elapsed_time(b))
+            ev.record(i, 1, stream)
+        torch.cuda.synchronize()
+        ts = [ev.elapsed_ms(i) for i in range(reps)]
+        ev.close()
         best = max(best, (nbytes / (statistics.median(ts) * 1e-3) / 1e9, per_cu))
     return best
 
@@ -293,8 +293,8 @@ def cpu_small_configs(O, threads, reps=5):
 # ------------------------------------------------------------------------------------------------ extras
 def _median_event_ms(fn, reps, rotate, calls=20):
     """Device time per call: `calls` calls (cycling over `rotate` buffer sets) are captured in one HIP
-    graph, the graph is replayed `reps` times between torch events on the current stream, and the
-    median replay time / calls is returned -- the host's per-call launch overhead is not in it."""
+    graph, the graph is replayed `reps` times between fence-free HIP events on the current stream, and
+    the median replay time / calls is returned -- the host's per-call launch overhead is not in it."""
     for i in range(rotate):
         fn(i)
     torch.cuda.synchronize()
@@ -310,13 +310,16 @@ def _median_event_ms(fn, reps, rotate, calls=20):
             fn(i % rotate)
     g.replay()
     torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
-        a.record()
+    ev = HipEvents(reps)
+    stream = torch.cuda.current_stream().cuda_stream
+    for i in range(reps):
+        ev.record(i, 0, stream)
         g.replay()
-        b.record()
+        ev.record(i, 1, stream)
     torch.cuda.synchronize()
-    return statistics.median(a.elapsed_time(b) for a, b in evs) / calls
+    ms = statistics.median(ev.elapsed_ms(i) for i in range(reps)) / calls
+    ev.close()
+    return ms
 
 
 def rw_floor(read_bytes, write_bytes, reps=20):
