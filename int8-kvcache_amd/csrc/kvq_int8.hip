@@ -2727,8 +2727,8 @@ int lds_prefetch_depth() {
   return depth;
 }
 
-// slots of verify_kernel's LDS ring (KVQ_V32_RING: 3 or 4; 3, 4 and 5 time the same on verification
-// batches, 6 is slower)
+// slots of verify_kernel's LDS ring (KVQ_V32_RING: 2, 3 or 4; 2 only with two key splits, where it is
+// the fastest on verification batches: 3 or 4 slots took 66.5-67 against 62-64 us on c3)
 int v32_ring_depth() {
   const char* e = getenv("KVQ_V32_RING");
   const int v = e ? atoi(e) : DEFAULT_V32_RING;
