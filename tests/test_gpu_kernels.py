@@ -141,8 +141,8 @@ def test_quant_cache_c1_full_size_bit_exact(qc_kernel):
 
 
 def test_quant_cache_rounding_boundaries(qc_kernel):
-    """Quotients on and within a few ulp of half-integers (the kernel's exact-division slow path),
-    and saturation: bit-exact against the IEEE C restatement."""
+    """Quotients on and within a few ulp of half-integers (where a rounding of x * (1/s) that is not
+    corrected to fl(x / s) would go wrong), and saturation: bit-exact against the IEEE C restatement."""
     r = synth.rng(2)
     n, H, D = 512, 4, 128
     k = torch.from_numpy(r.integers(-140, 140, (n, H, D)).astype(np.float32) + 0.5) * 0.25   # exact ties
@@ -158,6 +158,31 @@ def test_quant_cache_rounding_boundaries(qc_kernel):
         slots = torch.arange(n, dtype=torch.int64)
         ck.quant_reshape_and_cache(dev(key), dev(key), kc, vc, dev(slots), dev(st))
         ref = c_oracle.quant_rows(key, None, ks)
+        assert torch.equal(kc.cpu().reshape(n, H, D), ref)
+        assert torch.equal(vc.cpu().reshape(n, H, D), ref)
+
+
+
+def test_quant_cache_saturates_infinite_and_overflowing_quotients(qc_kernel):
+    """K/V rows holding +-inf, the largest bf16 values and ordinary values, with scales small enough that
+    x / s overflows to +-inf for some of them: every such code saturates to +-127, as IEEE division
+    then rint and the clamp give (the kernel clamps its first quotient estimate so that no NaN can
+    appear in the correction). Bit-exact against the C restatement and the torch oracle."""
+    r = synth.rng(5)
+    n, H, D = 64, 4, 128
+    x = r.standard_normal((n, H, D)).astype(np.float32) * 4
+    special = np.array([np.inf, -np.inf, 3.38e38, -3.38e38, 1e30, -1e30, 0.0, -0.0], dtype=np.float32)
+    idx = r.integers(0, n * H * D, 4096)
+    x.reshape(-1)[idx] = special[r.integers(0, len(special), idx.size)]
+    key = synth.bf16(x)
+    for s in (torch.full((H, D), 0.05), torch.full((H, D), 1e-30), torch.from_numpy(r.uniform(1e-3, 2.0, (H, D)).astype(np.float32))):
+        st = {"k_scale": s.contiguous(), "v_scale": s.contiguous(), "k_mu": torch.zeros(H, D)}
+        kc = torch.zeros(n // 16, 16, H, D, dtype=torch.int8, device=DEV)
+        vc = torch.zeros_like(kc)
+        slots = torch.arange(n, dtype=torch.int64)
+        ck.quant_reshape_and_cache(dev(key), dev(key), kc, vc, dev(slots), dev(st))
+        ref = c_oracle.quant_rows(key, None, s)
+        assert torch.equal(ref, O.quantize(key.float(), s)), "the two oracles agree"
         assert torch.equal(kc.cpu().reshape(n, H, D), ref)
         assert torch.equal(vc.cpu().reshape(n, H, D), ref)
 
