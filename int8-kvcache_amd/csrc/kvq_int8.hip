@@ -325,6 +325,9 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_WAV
 // still stores, through a descriptor with no records, which the hardware's range check drops; the
 // scales come from LDS at each token. The ring's waits then leave QC_ROW_PF - 1 tokens' loads and
 // the stores of earlier tokens in flight instead of draining them per token.
+#ifndef QC_ROW_BLOCK
+#define QC_ROW_BLOCK 256      // threads per workgroup of the wavefront-row kernel
+#endif
 #ifndef QC_ROW_PF
 #define QC_ROW_PF 4           // ring of token loads per wavefront (QC_ROW_PF - 1 in flight ahead)
 #endif
@@ -337,7 +340,7 @@ constexpr int QC_LOAD_AUX = QC_NT_LOAD ? 2 : 0;    // 2: nontemporal
 constexpr int QC_STORE_AUX = QC_NT_STORE ? 2 : 0;
 
 template <int D>
-__global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW_WAVES))) void quant_cache_rows_kernel(
+__global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW_WAVES))) void quant_cache_rows_kernel(
     const uint16_t* __restrict__ key, int key_st, int key_sh, int key_bytes, const uint16_t* __restrict__ value,
     int val_st, int val_sh, int val_bytes, int8_t* __restrict__ kc, int64_t kc_sb, int64_t kc_sn, int kc_sh,
     int8_t* __restrict__ vc, int64_t vc_sb, int64_t vc_sn, int vc_sh, int row_bytes, const int64_t* __restrict__ slots,
@@ -346,7 +349,7 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
   constexpr int LPH = D / QC_CPL;                 // lanes per head
   constexpr int HPW = WAVE / LPH;                 // heads per wavefront
   constexpr int CH = WAVE * QC_CPL;               // channels per wavefront
-  constexpr int WPB = QC_BLOCK / WAVE;
+  constexpr int WPB = QC_ROW_BLOCK / WAVE;
   // a workgroup owns one part (HPW heads) of WPB tokens at a time; the grid is a multiple of wpt
   const int part = blockIdx.x % wpt;
   const int lane = threadIdx.x % WAVE;
@@ -358,7 +361,7 @@ __global__ __launch_bounds__(QC_BLOCK) __attribute__((amdgpu_waves_per_eu(QC_ROW
   // wavefront of the grid reads the same few lines of these tables, so per-wavefront loads would pile
   // onto a few L2 channels, and a wavefront's own divisions would cost as much as its tokens' codes
   __shared__ float4 tab[5][CH / 4];  // k_scale, v_scale, k_mu, 1 / k_scale, 1 / v_scale of channels part * CH + c
-  for (int i = threadIdx.x; i < 3 * CH / 4; i += QC_BLOCK) {
+  for (int i = threadIdx.x; i < 3 * CH / 4; i += QC_ROW_BLOCK) {
     const int t = i / (CH / 4), c = (i % (CH / 4)) * 4, ch = part * CH + c;
     float4 v;
     if (t == 2) v = *reinterpret_cast<const float4*>(kmu + ch);
@@ -2761,7 +2764,7 @@ int device_cus() {
 
 // workgroups of 256 threads of kernel K resident per CU at once (queried once); the environment
 // variable `env`, when set to a positive count, overrides it on every call (a tuning and test knob)
-template <auto K>
+template <auto K, int THREADS = QC_BLOCK>
 int resident_blocks(const char* env) {
   if (const char* e = getenv(env)) {
     const int v = atoi(e);
@@ -2769,7 +2772,7 @@ int resident_blocks(const char* env) {
   }
   static const int nb = [] {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, QC_BLOCK, 0) != hipSuccess || v <= 0) v = QC_WAVES;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, K, THREADS, 0) != hipSuccess || v <= 0) v = QC_WAVES;
     return v;
   }();
   return nb;
@@ -2977,23 +2980,23 @@ int kvq_quant_cache(const void* key, int64_t key_st, int64_t key_sh, const void*
   if (!lanes_only && (num_heads * head_dim) % (WAVE * QC_CPL) == 0 && std::max({key_bytes, val_bytes, row_bytes}) <= INT32_MAX) {
     // whole wavefronts per token: the wavefront-row kernel; the grid holds a whole number of tokens'
     // wavefronts (wpt) and no more workgroups than are resident at once
-    // a workgroup owns one of the token's wpt parts for QC_BLOCK / WAVE tokens at a time (the grid
+    // a workgroup owns one of the token's wpt parts for QC_ROW_BLOCK / WAVE tokens at a time (the grid
     // is a multiple of wpt). Balanced: the fewest tokens per wavefront one resident round allows,
     // then just enough workgroups for n at that count -- a wavefront with fewer tokens than its
     // ring holds still issues (and drops) the rest
     const int wpt = (int)(num_heads * head_dim / (WAVE * QC_CPL));
-    const int wpb = QC_BLOCK / WAVE;
+    const int wpb = QC_ROW_BLOCK / WAVE;
     auto go = [&](auto kern, int resident) {
       const int64_t conc = std::max<int64_t>(1, (int64_t)device_cus() * resident / wpt) * wpb;  // tokens in flight
       const int64_t per = (n_tokens + conc - 1) / conc;                                        // tokens per wavefront
       const int64_t grid = (n_tokens + wpb * per - 1) / (wpb * per) * wpt;
-      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(QC_BLOCK), 0, st, (const uint16_t*)key, (int)key_st,
+      hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(QC_ROW_BLOCK), 0, st, (const uint16_t*)key, (int)key_st,
                          (int)key_sh, (int)key_bytes, (const uint16_t*)value, (int)val_st, (int)val_sh, (int)val_bytes,
                          k_cache, kc_sb, kc_sn, (int)kc_sh, v_cache, vc_sb, vc_sn, (int)vc_sh, (int)row_bytes,
                          slot_mapping, (int)n_tokens, wpt, num_slots, lbs, k_scale, ks_pc, v_scale, vs_pc, k_mu);
     };
-    if (head_dim == 128) go(quant_cache_rows_kernel<128>, resident_blocks<quant_cache_rows_kernel<128>>("KVQ_QC_WG_PER_CU"));
-    else go(quant_cache_rows_kernel<64>, resident_blocks<quant_cache_rows_kernel<64>>("KVQ_QC_WG_PER_CU"));
+    if (head_dim == 128) go(quant_cache_rows_kernel<128>, resident_blocks<quant_cache_rows_kernel<128>, QC_ROW_BLOCK>("KVQ_QC_WG_PER_CU"));
+    else go(quant_cache_rows_kernel<64>, resident_blocks<quant_cache_rows_kernel<64>, QC_ROW_BLOCK>("KVQ_QC_WG_PER_CU"));
     return launched("quant_cache");
   }
   if (num_heads * (head_dim / QC_CPL) > QC_BLOCK) return fail("quant_cache: at most %d heads of dim %lld", (int)(QC_BLOCK * QC_CPL / head_dim), (long long)head_dim);
