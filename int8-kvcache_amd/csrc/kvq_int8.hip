@@ -357,29 +357,51 @@ __global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC
   const int stride = (gridDim.x / wpt) * WPB;
   const int h = part * HPW + lane / LPH, d0 = (lane % LPH) * QC_CPL;
 
-  // the part's scales, k_mu and the scales' reciprocals (IEEE division), made once per workgroup: every
+  // The part's scales, k_mu and the scales' reciprocals (IEEE division), made once per workgroup: every
   // wavefront of the grid reads the same few lines of these tables, so per-wavefront loads would pile
-  // onto a few L2 channels, and a wavefront's own divisions would cost as much as its tokens' codes
+  // onto a few L2 channels, and a wavefront's own divisions would cost as much as its tokens' codes.
+  // Each thread requests its table entries first, then its wavefront's first tokens, and builds its
+  // entries once they (and only they: the loads return in order) have arrived; a barrier on LDS alone
+  // then publishes the table while the tokens are still in flight.
   __shared__ float4 tab[5][CH / 4];  // k_scale, v_scale, k_mu, 1 / k_scale, 1 / v_scale of channels part * CH + c
-  for (int i = threadIdx.x; i < 3 * CH / 4; i += QC_ROW_BLOCK) {
-    const int t = i / (CH / 4), c = (i % (CH / 4)) * 4, ch = part * CH + c;
-    float4 v;
-    if (t == 2) v = *reinterpret_cast<const float4*>(kmu + ch);
-    else {
-      const float* tb = t == 0 ? ks : vs;
-      if (t == 0 ? ks_pc : vs_pc) v = *reinterpret_cast<const float4*>(tb + ch);
-      else { const float x = tb[ch / D]; v = float4{x, x, x, x}; }   // 4 channels never straddle a head
-      tab[3 + t][i % (CH / 4)] = float4{1.f / v.x, 1.f / v.y, 1.f / v.z, 1.f / v.w};
+  constexpr int NTAB = 3 * CH / 4, TPT = (NTAB + QC_ROW_BLOCK - 1) / QC_ROW_BLOCK;
+  float tv[TPT][4];
+  auto table_loads = [&] {
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {  // branch-free: an index past the table re-reads its last entry
+      const int i = min((int)threadIdx.x + j * QC_ROW_BLOCK, NTAB - 1);
+      // the table a wavefront's entries belong to is uniform (CH / 4 entries per table, a multiple of 64)
+      const int t = __builtin_amdgcn_readfirstlane(i / (CH / 4)), ch = part * CH + (i % (CH / 4)) * 4;
+      // (two-way selects: a three-way choice among the kernel's pointers became a lookup table in
+      // scratch memory)
+      const float* sb = t == 0 ? ks : vs;
+      const bool spc = (t == 0 ? ks_pc : vs_pc) != 0;   // per head: the head's one scale (4 channels never straddle a head)
+      const float* e0 = t == 2 ? kmu + ch : (spc ? sb + ch : sb + ch / D);
+      const int step = (t == 2 || spc) ? 1 : 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) tv[j][k] = e0[k * step];
     }
-    tab[t][i % (CH / 4)] = v;
-  }
-  __syncthreads();
+  };
+  auto tables = [&] {
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const int i = (int)threadIdx.x + j * QC_ROW_BLOCK;
+      if (i < NTAB) {
+        const int t = i / (CH / 4);
+        tab[t][i % (CH / 4)] = float4{tv[j][0], tv[j][1], tv[j][2], tv[j][3]};
+        if (t < 2) tab[3 + t][i % (CH / 4)] = float4{1.f / tv[j][0], 1.f / tv[j][1], 1.f / tv[j][2], 1.f / tv[j][3]};
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // LDS writes done; token loads stay in flight
+  };
   // tokens of this wavefront: tpw consecutive ones from t0, so that each workgroup streams a
   // contiguous run of key / value rows (the interleaved order -- token t_first + k * stride -- timed
-  // 0.7% slower on c1)
-  const int tpw = (n + stride - 1) / stride, t0 = t_first * tpw;
-  if (t0 >= n) return;
-  const int steps = min(tpw, n - t0);
+  // 0.7% slower on c1). A wavefront past the last token still fetches (token n - 1, discarded) and
+  // meets the table's barrier before it leaves.
+  const int tpw = (n + stride - 1) / stride;
+  const bool live = t_first * tpw < n;
+  const int t0 = live ? t_first * tpw : n - 1;
+  const int steps = live ? min(tpw, n - t0) : 1;
   const int64_t bmask = (int64_t(1) << lbs) - 1;
   // per-lane byte offsets within a token's rows (all extents < 2^31 bytes: host)
   const int koff = 2 * (h * key_sh + d0), voff = 2 * (h * val_sh + d0);
@@ -425,13 +447,20 @@ __global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC
   if (steps <= QC_ROW_PF - 1) {
     // all of the wavefront's tokens in flight at once (entries past the last re-read it, and drop
     // their stores)
+    table_loads();
 #pragma unroll
     for (int j = 0; j < QC_ROW_PF - 1; ++j) fetch(j, j);
+    tables();
+    if (!live) return;
     prepare();
 #pragma unroll
     for (int j = 0; j < QC_ROW_PF - 1; ++j) emit(j, j < steps);
     return;
   }
+  // (with a ring, the table first: holding its entries across the first fetches spills registers; its
+  // latency is shared by more tokens here)
+  table_loads();
+  tables();
 #pragma unroll
   for (int j = 0; j < QC_ROW_PF - 1; ++j) fetch(j, j);
   prepare();
