@@ -105,8 +105,8 @@ def build_c2(B=128, L=32768, hq=28, hkv=4, d=128, bs=16):
 
 def backend_passes_split_buffers(q_lens, seq_lens, num_kv_heads):
     """Whether the vLLM backend hands the kernel its split buffers for this batch, outside graph capture
-    (kvq.vllm_int8.backend Int8StaticBuilder._split_for -> cuda_kernels.split_pays): not for enough
-    short-query requests of even length to fill the GPU in one pass."""
+    (kvq.vllm_int8.backend Int8StaticBuilder._split_for -> cuda_kernels.split_pays): not for short-query
+    requests of even length whose (request, kv head) pairs give every CU a whole number of them."""
     return ck.split_pays(np.asarray(q_lens), np.asarray(seq_lens), num_kv_heads, ck.one_pass_fill(DEV))
 
 
@@ -545,7 +545,7 @@ def main():
     torch.cuda.synchronize()
     print("# timing c2", file=sys.stderr, flush=True)
     # the call as the vLLM backend makes it for this batch outside graph capture: 128 requests x 4 kv heads
-    # of even length fill the GPU, so no split buffers (one pass); the call with split buffers (what a
+    # of even length give every CU two pairs, so no split buffers (one pass); the call with split buffers (what a
     # captured graph replays) is reported beside it
     split = backend_passes_split_buffers([1] * w["B"], [w["L"]] * w["B"], w["hkv"])
     # the other call is timed first, after 30 untimed calls (~20 ms): a GPU that has idled while the host
@@ -569,8 +569,8 @@ def main():
                                "d128, block 16, vLLM interleaved int8 cache, shuffled block tables",
                    "split_buffers": split, "max_splits": splits,
                    "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch outside "
-                           "graph capture (enough requests of even length to fill the GPU: no split buffers, one "
-                           "pass, nothing allocated)" if not split else
+                           "graph capture (requests of even length, two (request, kv head) pairs per CU: no split "
+                           "buffers, one pass, nothing allocated)" if not split else
                            "kvq.cuda_kernels.decode_attention with split buffers, as the vLLM backend calls it",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / (launch_ms * 1e-3) / 1e9, 1), "peak": PEAK_GBS,

@@ -264,26 +264,33 @@ def split_buffers(num_tokens, num_q_heads, head_dim, splits, device):
 
 SPLIT_PIECES = 16        # pieces per (request, kv head) of the vLLM backend's split buffers (as vLLM's own)
 EVEN_LENGTHS = 1.05      # a batch whose longest short request is within this factor of the mean is even
+ROUND_SLACK = 1.1        # one pass: the busiest CU's whole pairs at most this far above an even share
 
 
 def one_pass_fill(device):
-    """(request, kv head) pairs that fill the device in one pass: two workgroups per CU."""
+    """The CUs: a call without split buffers runs one workgroup per CU, each streaming whole (request,
+    kv head) pairs in turn."""
     dev = torch.device(device)
-    return 2 * (torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 256)
+    return torch.cuda.get_device_properties(dev).multi_processor_count if dev.type == "cuda" else 256
 
 
 def split_pays(query_lens, seq_lens, num_kv_heads, fill):
     """Whether split buffers pay for a batch, from host-side lengths (numpy; seq_lens None = unknown): with
     them the kernel cuts the longest (request, kv head) pairs across workgroups and merges the pieces in
-    a second launch; without, each pair runs whole in one workgroup. One pass serves as well only when
-    the short-query requests (1..SHORT_Q tokens) give at least `fill` pairs and their lengths are within
+    a second launch; without, each pair runs whole in one of `fill` workgroups (one per CU). One pass
+    serves as well only when the short-query requests (1..SHORT_Q tokens) give at least `fill` pairs,
+    whole pairs spread over the CUs within ROUND_SLACK of evenly (1, 2, 3, 4 pairs per CU, not 1.5 or
+    2.5: there the busiest CUs stream a pair more than the rest), and their lengths are within
     EVEN_LENGTHS of even. False when no request has a short query."""
     q = np.asarray(query_lens)
     short = (q >= 1) & (q <= SHORT_Q)
     n = int(short.sum())
     if n == 0:
         return False
-    if seq_lens is None or n * num_kv_heads < fill:
+    pairs = n * num_kv_heads
+    if seq_lens is None or pairs < fill:
+        return True
+    if -(-pairs // fill) * fill > ROUND_SLACK * pairs:
         return True
     ls = np.asarray(seq_lens)[:len(q)][short].astype(np.int64)
     return int(ls.max()) * n > EVEN_LENGTHS * int(ls.sum())

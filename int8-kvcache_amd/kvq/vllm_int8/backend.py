@@ -27,7 +27,8 @@ cut pieces go to split buffers that the builder allocates once, sized for the sh
 full batch (vLLM's own split buffers hold only 128 // kv-heads requests' rows, and the reference passes
 them only to batches that small). Short-query requests are ordered first (reorder_batch_threshold), so
 their tokens are the buffers' rows. Each step the builder passes them unless the batch is one that a
-single pass serves as well: enough requests to fill the GPU and lengths within 5% of even.
+single pass serves as well: requests whose (request, kv head) pairs fill every CU with a whole number
+of pairs each (one workgroup per CU streams them in turn) and lengths within 5% of even.
 Full graphs are offered only for uniform batches the INT8 kernel covers alone (the long-query path sizes
 buffers from host-side lengths).
 """
@@ -186,7 +187,7 @@ class Int8StaticBuilder(TritonAttentionMetadataBuilder):
 
     def _split_for(self, c, capturing=False):
         """The split buffers for this step, or None where one pass serves as well (cuda_kernels.split_pays:
-        enough short-query requests to fill the GPU, host-side lengths even). A graph being captured always
+        short-query requests whose pairs fill the CUs evenly, host-side lengths even). A graph being captured always
         gets them: its replays see other lengths, and the kernel cuts only what the lengths it reads on
         the device call for."""
         if self.kvq_segm is None:

@@ -36,8 +36,9 @@ BATCHES = {
     # skewed decode batch with more short tokens than the buffers' 64 rows
     "many_decode": ([1] * 90 + [5, 20, 3], [int(x) for x in synth.rng(5).integers(1, 4000, 90)] + [9000, 700, 300],
                     True),
-    # enough requests to fill the GPU (x 4 kv heads >= 2 per CU), even lengths: one pass
-    "many_even": ([1] * 140, [1500] * 140, False),
+    # requests whose pairs give every CU a whole number of them (x 4 kv heads = 2 per CU), even lengths:
+    # one pass
+    "many_even": ([1] * 128, [1500] * 128, False),
 }
 
 

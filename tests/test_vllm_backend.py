@@ -228,15 +228,20 @@ def test_builder_split_buffers_cover_a_full_batchs_short_tokens(tmp_path, monkey
 
 
 def test_builder_passes_split_buffers_unless_one_pass_serves(tmp_path, monkeypatch):
-    """Per step: split buffers for batches with too few (request, kv head) pairs to fill the GPU, for
-    skewed lengths and when host lengths are unknown; none for many requests of even length, or when no
-    request has a short query. A graph being captured always gets them."""
-    b = _split_builder(tmp_path, monkeypatch, max_num_seqs=256)
-    assert b.kvq_fill == 512 and backend.Int8StaticBuilder.reorder_batch_threshold == ck.SHORT_Q
-    n = b.kvq_fill // HKV                                     # requests that fill the GPU
+    """Per step: split buffers for batches with too few (request, kv head) pairs to give every CU one,
+    with pairs that spread over the CUs unevenly (1.5, 2.5 per CU), for skewed lengths and when host
+    lengths are unknown; none for requests of even length that give every CU a whole number of pairs,
+    or when no request has a short query. A graph being captured always gets them."""
+    b = _split_builder(tmp_path, monkeypatch, max_num_seqs=1024)
+    assert b.kvq_fill == 256 and backend.Int8StaticBuilder.reorder_batch_threshold == ck.SHORT_Q
+    n = b.kvq_fill // HKV                                     # requests whose pairs give every CU one
     even = torch.full((n,), 4096, dtype=torch.int32)
     assert b.build(0, _common([1] * (n - 1), [4096] * (n - 1), upper=even[:n - 1])).kvq_segm is b.kvq_segm
     assert b.build(0, _common([1] * n, [4096] * n, upper=even)).kvq_segm is None
+    for per_cu, split in ((1.5, True), (2, False), (2.5, True), (3, False), (4, False)):
+        m = int(per_cu * n)
+        assert (b.build(0, _common([1] * m, [4096] * m, upper=torch.full((m,), 4096, dtype=torch.int32))).kvq_segm
+                is b.kvq_segm) == split, per_cu
     nearly = even.clone()
     nearly[0] = 4300                                          # max / mean just under 1.05: still even
     assert b.build(0, _common([1] * n, nearly.tolist(), upper=nearly)).kvq_segm is None
