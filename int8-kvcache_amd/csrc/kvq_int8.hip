@@ -761,8 +761,11 @@ __device__ __forceinline__ void transpose4x4(uint32_t a0, uint32_t a1, uint32_t 
 // denominator and accumulators in slot (k - 1) * rt + t, lane-major ([field][lane]: conflict-free).
 constexpr int MERGE_FIELDS = 36;  // 32 accumulators (D = 128), max, denominator, 2 spare
 constexpr int MERGE_SLOTS = MAX_ROW_TILES - 1;
+// Shortest piece split across a workgroup's key splits, in tiles per key split: shorter pieces go
+// whole to one key split in turn (no barrier, no merge). c4's decode rows: 2, 3, 4 all 117.8-118.0 us,
+// 6 119.0, 8 119.3, 16 121.9 us.
 #ifndef KVQ_COOP_TILES
-#define KVQ_COOP_TILES 8
+#define KVQ_COOP_TILES 4
 #endif
 constexpr int COOP_TILES = KVQ_COOP_TILES;
 constexpr float ATTN_SLACK = 8.f;  // log2 headroom of the attention's reference maximum
