@@ -24,6 +24,23 @@ def record(test, **metrics):
             f.write(json.dumps({"test": test, **metrics}) + "\n")
 
 
+def q_code_flips(c):
+    """[T, Hq] bool for a golden case: rows whose q codes differ between the kernel's fp32 q arithmetic
+    (q' = fl32(q * s_k), fp32 scale and quotient) and int8_ref's fp64 one (kvq/int8_ref.py:108-115 with
+    kvq/quant.py:46-51): bf16 q puts quotients on exact rounding ties, which the two break differently."""
+    import torch
+    from oracle import kvq_oracle as O
+
+    q, ks = c["q"], c["static"]["k_scale"]
+    ksr = ks.repeat_interleave(q.shape[1] // ks.shape[0], 0)  # [Hq, D | 1]
+    per_channel = ks.shape[-1] > 1
+    codes = []
+    for dt in (torch.float32, torch.float64):
+        x = q.to(dt) * ksr.to(dt) if per_channel else q.to(dt)
+        codes.append(O.quantize(x, O.scale_from_absmax(x.abs().amax(-1, keepdim=True))))
+    return (codes[0] != codes[1]).any(-1)
+
+
 def nan_like(t):
     """An output buffer that starts as NaN, so a row a kernel fails to write cannot pass a check."""
     import torch

@@ -9,7 +9,7 @@ import os
 import numpy as np
 import pytest
 import torch
-from conftest import nan_like, nan_segm, record
+from conftest import nan_like, nan_segm, q_code_flips, record
 
 import cases
 from oracle import c_oracle
@@ -222,8 +222,16 @@ def test_attention_matches_reference_golden(golden, name):
     short = short_rows(c["cu"])[rows]
     ref = g[f"{name}|int8_b"]                      # the reference's B (fp64 q rounding), bf16
     e = O.compare(ref[short], o[short])
-    record("golden_int8_b", case=name, **e)
-    assert e["rel_l2"] < REL_L2, e
+    # rows whose q codes the fp32 q contract and int8_ref's fp64 q rounding break differently
+    # (test_oracle_fp32_q_matches_golden_off_flipped_rows: the oracle's fp32 variant deviates there alike)
+    flips = q_code_flips(c)[rows][short]
+    dev_row = (o[short].float() - ref[short].float()).abs().amax(-1)
+    e_flip = float(dev_row[flips].max()) if flips.any() else 0.0
+    record("golden_int8_b", case=name, flipped_rows=int(flips.sum()), max_abs_flipped=e_flip, **e)
+    # against the reference's own fp64-q output: its rel_l2 bar and the strict mean bar over every short
+    # row, the strict max bar on every row whose q codes agree
+    assert e["rel_l2"] < REL_L2 and e["mean_abs"] <= ATOL_MEAN, e
+    assert float(dev_row[~flips].max()) <= ATOL_MAX, (float(dev_row[~flips].max()), e)
     strict = oracle_attention(c, kq, vq, c["per_channel"])[rows]
     check_attention(strict[short], o[short], "golden_case_vs_fp32q_oracle", case=name)
     if (~short).any():
