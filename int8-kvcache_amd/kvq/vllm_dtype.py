@@ -195,6 +195,15 @@ def install(root=None):
     return written
 
 
+def missing_tables(root=None):
+    """Paths (relative to the vllm package) of the tables that still lack int8_static, or None when
+    `root` (default: the importable vllm) is not a source tree with these tables."""
+    try:
+        return [FILES[key] for key, ok in status(root).items() if not ok]
+    except PatchError:
+        return None
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog="python -m kvq.vllm_dtype", description=__doc__.split("\n\n")[0])
     ap.add_argument("--vllm-root", help="vllm package directory (default: the one `import vllm` loads)")

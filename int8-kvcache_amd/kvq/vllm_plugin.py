@@ -8,7 +8,8 @@ Install this package where vLLM's workers import from, with an entry point in th
 
 vLLM calls register() in every process it starts, before the model is built: it registers the static
 INT8 backend as AttentionBackendEnum.CUSTOM (by class path, so the backend module is imported only
-when vLLM selects it) and, with KVQ_CAPTURE=1, wraps the bf16 attention backend to record the K/V
+when vLLM selects it), warns when the installed vLLM does not know kv_cache_dtype="int8_static" yet
+(kvq.vllm_dtype registers it) and, with KVQ_CAPTURE=1, wraps the bf16 attention backend to record the K/V
 statistics that calibration turns into static scales (kvq.capture).
 """
 import os
@@ -18,6 +19,15 @@ def register():
     from vllm.v1.attention.backends.registry import AttentionBackendEnum, register_backend
 
     register_backend(AttentionBackendEnum.CUSTOM, "kvq.vllm_int8.backend.Int8StaticBackend")
+    from kvq import vllm_dtype
+
+    missing = vllm_dtype.missing_tables()
+    if missing:  # vLLM would reject kv_cache_dtype="int8_static" before asking any backend
+        from vllm.logger import init_logger
+
+        init_logger(__name__).warning(
+            "kv_cache_dtype int8_static is not registered in this vLLM (%s); run `python -m kvq.vllm_dtype` once",
+            ", ".join(missing))
     if os.environ.get("KVQ_CAPTURE") == "1":
         from kvq import capture
 

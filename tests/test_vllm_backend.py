@@ -64,6 +64,26 @@ def test_plugin_registers_custom_backend_by_class_path():
     assert backend_cls.customize_spec(spec) is spec
 
 
+def test_plugin_warns_while_int8_static_is_unregistered(tmp_path, monkeypatch, caplog):
+    """register() names the fix when the installed vLLM would reject kv_cache_dtype="int8_static", and is
+    quiet once kvq.vllm_dtype has registered it (a vLLM-shaped tree stands in for the installed vLLM)."""
+    import logging
+
+    from kvq import vllm_dtype
+    from test_vllm_dtype import make_tree
+
+    pkg = make_tree(tmp_path)
+    monkeypatch.setattr(vllm_dtype, "find_vllm", lambda: pkg)
+    with caplog.at_level(logging.WARNING):
+        vllm_plugin.register()
+    assert "python -m kvq.vllm_dtype" in caplog.text and "config/cache.py" in caplog.text
+    caplog.clear()
+    vllm_dtype.install(pkg)
+    with caplog.at_level(logging.WARNING):
+        vllm_plugin.register()
+    assert "int8_static" not in caplog.text
+
+
 def test_plugin_refuses_study_paths_it_does_not_ship(monkeypatch):
     monkeypatch.setenv("KVQ_ATTN", "B_channel")
     with pytest.raises(RuntimeError, match="KVQ_ATTN"):

@@ -4,7 +4,6 @@ each test writes a small vLLM-shaped package (the three tables, laid out as vLLM
 registers the dtype, imports the edited modules and checks what vLLM would see: the name in the
 CacheDType Literal, torch.int8 as its cache dtype, a new KVQuantMode member past the existing ones and
 the string -> mode mapping, with every earlier mapping unchanged."""
-import enum
 import importlib.util
 import os
 import typing
@@ -161,3 +160,11 @@ def test_cli_check_and_install(tmp_path, capsys):
     assert vd.main(["--vllm-root", pkg]) == 0
     assert vd.main(["--vllm-root", pkg, "--check"]) == 0
     assert vd.main(["--vllm-root", str(tmp_path)]) == 2
+
+
+def test_missing_tables_names_what_the_plugin_warns_about(tmp_path):
+    pkg = make_tree(tmp_path)
+    assert vd.missing_tables(pkg) == list(vd.FILES.values())
+    vd.install(pkg)
+    assert vd.missing_tables(pkg) == []
+    assert vd.missing_tables(str(tmp_path)) is None     # not a vLLM source tree: the plugin stays quiet
