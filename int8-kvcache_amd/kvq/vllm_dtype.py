@@ -85,7 +85,7 @@ def _append_entry(text, header, entry, present, where):
     if re.search(present, body):
         return text
     if "\n" not in body:
-        sep = "" if not body.strip() or body.rstrip().endswith(",") else ", "
+        sep = "" if not body.strip() else " " if body.rstrip().endswith(",") else ", "
         return text[:close_i].rstrip() + sep + entry + text[close_i:]
     lines = body.split("\n")
     code_lines = [i for i, ln in enumerate(lines) if ln.strip() and not ln.strip().startswith("#")]

@@ -140,6 +140,11 @@ def test_one_line_tables_and_no_trailing_comma(tmp_path):
     assert typing.get_args(load(pkg, "cache_dtype", "one").CacheDType) == ("auto", "fp8", "int8_static")
     assert load(pkg, "torch_dtype", "one").STR_DTYPE_TO_TORCH_DTYPE == {
         "half": torch.half, "fp8": torch.uint8, "int8_static": torch.int8}
+    with open(os.path.join(pkg, vd.FILES["cache_dtype"])) as f:
+        assert 'Literal["auto", "fp8", "int8_static"]' in f.read()
+    pkg2 = make_tree(tmp_path / "trailing", cache='from typing import Literal\nCacheDType = Literal["auto",]\n')
+    vd.install(pkg2)
+    assert typing.get_args(load(pkg2, "cache_dtype", "trail").CacheDType) == ("auto", "int8_static")
 
 
 def test_missing_table_writes_nothing(tmp_path):
