@@ -2012,6 +2012,7 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
 // -2 - l, a row that was not cut has -1 in slot 0 and was written by the attention kernel), so the
 // merge needs neither the plan nor any buffer beyond the split buffers of the call.
 constexpr int RED_WAVES = 4;
+constexpr int MERGE_Z = 64;   // largest z extent of split_reduce_kernel's grid
 template <int D>
 __device__ __forceinline__ void merge_row(const AttnArgs& a, int tok, int t, int h, int lane) {
   // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
@@ -3151,20 +3152,22 @@ int kvq_int8_decode_attention_noalloc(const void* q, int64_t q_st, int64_t q_sh,
                                       double softmax_scale, int64_t num_splits, int64_t target_waves,
                                       int64_t max_query_len, int64_t qmax, void* stream) {
   if (num_splits < 1 || num_splits > MAX_SPLITS) return fail("int8_decode_attention_noalloc: at most %d split-KV segments", MAX_SPLITS);
-  if (num_tokens < 0 || num_q_heads <= 0 || (head_dim != 64 && head_dim != 128))
+  // (the head count is bounded here, before any product of sizes: decode_attention bounds it again)
+  if (num_tokens < 0 || num_q_heads <= 0 || num_q_heads > 65535ll * RED_WAVES || (head_dim != 64 && head_dim != 128))
     return fail("int8_decode_attention_noalloc: bad sizes T=%lld Hq=%lld D=%lld", (long long)num_tokens,
                 (long long)num_q_heads, (long long)head_dim);
   float *so = nullptr, *sm = nullptr, *ss = nullptr;
   int64_t st_t = 0, st_h = 0;
   if (num_splits > 1) {
-    // [T, Hq, S, D] partial outputs, then [T, Hq, S] maxima and [T, Hq, S] denominators
-    const int64_t rows = num_tokens * num_q_heads * num_splits;
-    const int64_t need = rows * (head_dim + 2) * (int64_t)sizeof(float);
-    if (num_tokens > INT32_MAX || need > (int64_t)NOALLOC_SCRATCH_BYTES)
-      return fail("int8_decode_attention_noalloc: %lld tokens x %lld q heads x %lld splits need %lld bytes of split "
-                  "partials, more than the library's %lld-byte scratch; pass fewer splits (1 needs none)",
-                  (long long)num_tokens, (long long)num_q_heads, (long long)num_splits, (long long)need,
+    // [T, Hq, S, D] partial outputs, then [T, Hq, S] maxima and [T, Hq, S] denominators: compared by
+    // division, so no product of caller sizes can overflow
+    const int64_t per_token = num_q_heads * num_splits * (head_dim + 2) * (int64_t)sizeof(float);  // < 2^38
+    if (num_tokens > INT32_MAX || num_tokens > (int64_t)NOALLOC_SCRATCH_BYTES / per_token)
+      return fail("int8_decode_attention_noalloc: %lld tokens x %lld q heads x %lld splits need %lld bytes per token "
+                  "of split partials, more than the library's %lld-byte scratch holds; pass fewer splits (1 needs none)",
+                  (long long)num_tokens, (long long)num_q_heads, (long long)num_splits, (long long)per_token,
                   (long long)NOALLOC_SCRATCH_BYTES);
+    const int64_t rows = num_tokens * num_q_heads * num_splits;
     char* base = scratch_ptr();
     if (!base) return KVQ_ERR_LAUNCH;  // g_err set by scratch_ptr
     so = reinterpret_cast<float*>(base);
@@ -3229,7 +3232,7 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   const int v32ks = rows32 ? v32_key_splits() : 1;
   const int waves = rows32 ? 2 * v32ks : rt * ks;
   if (num_seqs > INT32_MAX - 1 || num_kv_heads > 65535 || (num_q_heads + RED_WAVES - 1) / RED_WAVES > 65535 ||
-      maxq > 65535)
+      (int64_t)G * maxq > INT32_MAX / 2)
     return fail("int8_decode_attention: grid too large");
   AttnArgs a;
   a.q = (const uint16_t*)q; a.kc = k_cache; a.vc = v_cache; a.out = (uint16_t*)out;
@@ -3307,7 +3310,10 @@ int decode_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_
   int rc = launched("int8_decode_attention");
   if (ev1) (void)hipEventRecord(ev1, st);
   if (rc != KVQ_OK || num_splits == 1 || a.cut_rows == 0) return rc;
-  const dim3 rgrid((unsigned)num_seqs, (unsigned)((num_q_heads + RED_WAVES - 1) / RED_WAVES), (unsigned)maxq);
+  // the merge's z blocks stride over a request's query tokens (split_reduce_kernel), so any query length
+  // is covered with at most MERGE_Z of them
+  const dim3 rgrid((unsigned)num_seqs, (unsigned)((num_q_heads + RED_WAVES - 1) / RED_WAVES),
+                   (unsigned)std::min<int64_t>(maxq, MERGE_Z));
   if (head_dim == 128) hipLaunchKernelGGL(split_reduce_kernel<128>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
   else hipLaunchKernelGGL(split_reduce_kernel<64>, rgrid, dim3(WAVE * RED_WAVES), 0, st, a);
   return launched("split_reduce");

@@ -61,6 +61,25 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc == 1 and b"scale columns" in lib.kvq_last_error()
 
 
+def test_noalloc_rejects_oversized_calls_before_any_device_call():
+    """kvq_int8_decode_attention_noalloc checks its sizes before it looks up its device array: head counts
+    beyond the merge grid's, and partials beyond the array, compared by division -- sizes whose product
+    would overflow 64 bits (2^31 - 1 tokens x 262,140 q heads x 64 splits x 130 floats) are rejected, not
+    wrapped into a small number."""
+    lib = _native.load()
+    nul = None
+
+    def call(T, hq, S, d=128):
+        return lib.kvq_int8_decode_attention_noalloc(nul, 0, 0, T, nul, 0, 0, 0, nul, 0, 0, 0, 64, 16, 4, d, nul, 0, 0,
+                                                     nul, nul, nul, 0, 1, hq, nul, d, nul, d, 0.1, S, 0, 1, 8, nul)
+    assert call(8, 65535 * 4 + 1, 1) == 1 and b"bad sizes" in lib.kvq_last_error()
+    assert call(2 ** 31 - 1, 65535 * 4, 64) == 1 and b"scratch holds" in lib.kvq_last_error()
+    assert call(2 ** 31 - 1, 28, 2) == 1 and b"scratch holds" in lib.kvq_last_error()
+    per_token = 28 * 16 * 130 * 4
+    assert call(lib.kvq_noalloc_scratch_bytes() // per_token + 1, 28, 16) == 1
+    assert b"scratch holds" in lib.kvq_last_error()
+
+
 def test_native_call_raises_with_message():
     with pytest.raises(_native.NativeError, match="head_dim must be 64 or 128"):
         _native.call("kvq_dequant_pages", None, 0, 0, 0, None, 0, 0, 0, 10, 16, 4, 96, None, None, None, 0, None,
