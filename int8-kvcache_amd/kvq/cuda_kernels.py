@@ -399,7 +399,8 @@ def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table
     paged prefill attention over it (reference kvq/cuda_kernels.py:106-131, which calls vLLM's
     FlashAttention with block_table = plan.block_table). Only the long requests' rows are written;
     short requests are left to decode_attention. The key counts are read on the device (seq_lens), the
-    plan's host lengths only size the temporary cache and order the work."""
+    plan's host lengths only size the temporary cache and order the work. KVQ_DEBUG_DUMP=path saves the
+    prefill call's metadata there first (kvq.debug_dump; the reference's dump, kvq/cuda_kernels.py:123-127)."""
     bs, h, d = k_cache.shape[1:]
     _check(bs == plan.block_size, f"block size {bs} != plan block size {plan.block_size}")
     src_req, src_j, bt_tmp = plan.gpu(q.device)
@@ -407,6 +408,10 @@ def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table
     vt = torch.empty_like(kt)
     ext().dequant_pages(k_cache, v_cache, kt, vt, block_table, src_req, src_j, static["k_scale"], static["v_scale"])
     tile_req, tile_row = plan.tiles(q.shape[1] // h, q.device)
+    if os.environ.get("KVQ_DEBUG_DUMP"):  # the prefill call's metadata, for an offline replay (kvq.debug_dump)
+        from . import debug_dump
+        debug_dump.dump_long_call(os.environ["KVQ_DEBUG_DUMP"], q, out, cu_seqlens_q, seq_lens, plan, kt, tile_req,
+                                  tile_row, max_query_len, ext().prefill_rows, softmax_scale)
     ext().paged_prefill_attention(q, kt, vt, out, cu_seqlens_q, seq_lens, bt_tmp, tile_req, tile_row, softmax_scale)
     return out
 
