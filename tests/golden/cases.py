@@ -28,6 +28,10 @@ def build(name):
     if name in ("c0_pc", "c0_ph"):
         c = synth.c0_case(per_channel=name == "c0_pc")
         c["per_channel"] = name == "c0_pc"
+    elif name == "c0_pc_nomu":
+        # config c0 as BASELINE.json states it: static per-channel scales, k_mu = 0 (no smooth-K)
+        c = synth.c0_case(per_channel=True, smooth=False)
+        c["per_channel"] = True
     elif name in ("short_28_4", "short_14_2_d64", "short_32_8_ph"):
         hq, hkv, d = {"short_28_4": (28, 4, 128), "short_14_2_d64": (14, 2, 64), "short_32_8_ph": (32, 8, 128)}[name]
         c = synth.paged_case(hq, hkv, *SHORT, head_dim=d, seed=21, dist="randn", scale=3.0)
@@ -47,8 +51,8 @@ def build(name):
     return c
 
 
-NAMES = ["c0_pc", "c0_ph", "short_28_4", "short_14_2_d64", "short_32_8_ph", "edge", "mixed"]
-WITH_BF16_REF = ["c0_pc", "c0_ph", "short_28_4", "mixed"]
+NAMES = ["c0_pc", "c0_pc_nomu", "c0_ph", "short_28_4", "short_14_2_d64", "short_32_8_ph", "edge", "mixed"]
+WITH_BF16_REF = ["c0_pc", "c0_pc_nomu", "c0_ph", "short_28_4", "mixed"]
 # cases also stored with q scales per 32 channels (int8_ref Cfg(q_gran="group32"), per-channel K)
 WITH_QGROUP32 = ["c0_pc", "short_28_4", "short_14_2_d64", "mixed"]
 

@@ -45,10 +45,11 @@ def main():
         st = c["static"]
         kq = ref_quant.quantize(c["k"].float() - st["k_mu"], st["k_scale"])
         vq = ref_quant.quantize(c["v"], st["v_scale"])
+        smooth = bool(st["k_mu"].abs().max() > 0)   # (an INT8 cache already holds k - mu: B does not read it)
         if c["per_channel"]:
-            cfg = ref_int8.Cfg(smooth_k=True, p_tile=32)
+            cfg = ref_int8.Cfg(smooth_k=smooth, p_tile=32)
         else:
-            cfg = ref_int8.Cfg(smooth_k=True, p_tile=32, k_gran="per_head", v_gran="per_head")
+            cfg = ref_int8.Cfg(smooth_k=smooth, p_tile=32, k_gran="per_head", v_gran="per_head")
         args = (c["cu"], c["seq_lens"], c["block_table"])
         b = ref_int8.paged_static_attention(cfg, st, cache_is_int8=True, short_q=8)(c["q"], kq, vq, *args, c["scale"])
         g = ref_attn.paged_attention_ref(c["q"], c["k"], c["v"], *args, c["scale"]) if name in cases.WITH_BF16_REF else None

@@ -131,8 +131,10 @@ def _interleaved(nb, hkv, bs, d):
 
 def test_c2_full_size_sampled_parity():
     """c2: 128 requests x 32768 keys in vLLM's interleaved cache, filled through the quantize-and-cache
-    kernel. Checks: the fill's codes for a sample of blocks are bit-exact; 6 sampled requests match the
-    oracle with split buffers (bench.py's step); the output without them (one pass, nothing cut) agrees."""
+    kernel. Checks: the fill's codes for a sample of blocks are bit-exact; 16 requests spread over the
+    batch (so over the stream-K workers' ranges: every 9th request from the 4th, and the first and last)
+    match the oracle with split buffers (a captured graph's call: segments cut once, a second kernel
+    merges); the output without them (bench.py's one pass, nothing cut) agrees."""
     B, L, hq, hkv, d, bs = 128, 32768, 28, 4, 128, 16
     pages = L // bs
     nb = B * pages + 64
@@ -152,7 +154,7 @@ def test_c2_full_size_sampled_parity():
     sl = torch.full((B,), L, dtype=torch.int32, device=DEV)
     out = ck.decode_attention(q, kc, vc, nan_like(q), cu, sl, bt, SCALE, st,
                               segm=nan_segm(B, hq, ck.choose_splits(bt.shape[1] * bs), d))
-    for r in (0, 17, 63, 64, 100, 127):
+    for r in sorted({0, 127} | set(range(3, 128, 9))):
         ref = _request_oracle(kc, vc, bt, r, L, q[r:r + 1], st)
         err = O.compare(ref, out[r:r + 1].cpu())
         record("c2_sampled", request=r, **err)
