@@ -5,9 +5,12 @@ Headline (BASELINE.json metric, config c2): INT8 paged decode attention, 128 req
 28 q / 4 kv heads, head_dim 128, block 16, in vLLM's interleaved [nb, H, bs, 2D] int8 cache (filled
 with c0-distribution codes by this package's quantize-and-cache kernel), shuffled block tables over
 263,168 blocks. A step is one kvq.cuda_kernels.decode_attention call made as the vLLM backend makes it
-for this batch -- 128 requests are more than vLLM's split buffers serve (128 // 4 kv heads), so none are
-passed: one pass, nothing allocated -- with every input resident in HBM. The same call with split
-buffers allocated once beforehand (attention kernel + split merge) is reported beside it.
+for this batch when it runs eagerly or under piecewise graphs: its per-step split rule
+(cuda_kernels.split_pays) sees 128 requests x 4 kv heads of equal length, two whole (request, kv head)
+pairs per CU, and passes no split buffers -- one pass, nothing cut, nothing allocated -- with every input
+resident in HBM. Under vLLM's full-graph decode (the backend declares UNIFORM_BATCH) a captured graph
+always carries the backend's split buffers, since its replays see other lengths; that call (attention
+kernel + split merge) is timed beside it as c2_other_call.
 
 Prints ONE JSON line. `value` is algorithmic bytes / step time (GB/s); `roofline` times the attention
 kernel alone with HIP events recorded around it on its own stream; `cpu_baseline` times the CPU oracle
@@ -568,9 +571,10 @@ def main():
         "config": {"workload": "c2: INT8 paged decode attention, 128 requests x 32768 keys, 28 q / 4 kv heads, "
                                "d128, block 16, vLLM interleaved int8 cache, shuffled block tables",
                    "split_buffers": split, "max_splits": splits,
-                   "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch outside "
-                           "graph capture (requests of even length, two (request, kv head) pairs per CU: no split "
-                           "buffers, one pass, nothing allocated)" if not split else
+                   "call": "kvq.cuda_kernels.decode_attention as the vLLM backend calls it for this batch eagerly "
+                           "or under piecewise graphs (requests of even length, two (request, kv head) pairs per CU: "
+                           "no split buffers, one pass, nothing allocated); a full-graph replay carries the split "
+                           "buffers: c2_other_call" if not split else
                            "kvq.cuda_kernels.decode_attention with split buffers, as the vLLM backend calls it",
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(alg / (launch_ms * 1e-3) / 1e9, 1), "peak": PEAK_GBS,

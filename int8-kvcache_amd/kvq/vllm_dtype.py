@@ -181,26 +181,44 @@ def status(root=None):
 
 def install(root=None):
     """Register int8_static in the vLLM package in `root` (default: the importable one). Returns the
-    paths written (empty when it was already registered)."""
+    paths written (empty when it was already registered). All or nothing: every edited file is written
+    to a temporary file beside it first; only then are they moved into place, and if any step fails the
+    temporary files are removed and the files already replaced get their original text back, so vLLM is
+    never left with some of its tables registered."""
     root = root or find_vllm()
-    written = []
-    for path, old, new in _plan(root).values():
-        if new == old:
-            continue
-        tmp = path + ".kvq-tmp"
-        with open(tmp, "w", encoding="utf-8") as f:
-            f.write(new)
-        os.replace(tmp, path)
-        written.append(path)
-    return written
+    todo = [(path, old, new) for path, old, new in _plan(root).values() if new != old]
+    staged, replaced = [], []
+    try:
+        for path, old, new in todo:
+            tmp = path + ".kvq-tmp"
+            staged.append(tmp)
+            with open(tmp, "w", encoding="utf-8") as f:
+                f.write(new)
+        for (path, old, new), tmp in zip(todo, staged):
+            _replace(tmp, path)
+            replaced.append((path, old))
+    except BaseException:
+        for tmp in staged:
+            if os.path.exists(tmp):
+                os.remove(tmp)
+        for path, old in replaced:
+            with open(path, "w", encoding="utf-8") as f:
+                f.write(old)
+        raise
+    return [path for path, _, _ in todo]
+
+
+def _replace(src, dst):
+    os.replace(src, dst)
 
 
 def missing_tables(root=None):
     """Paths (relative to the vllm package) of the tables that still lack int8_static, or None when
-    `root` (default: the importable vllm) is not a source tree with these tables."""
+    `root` (default: the importable vllm) is not a source tree with these tables, or its files cannot be
+    read or parsed (the plugin only warns: nothing here may stop vLLM from loading it)."""
     try:
         return [FILES[key] for key, ok in status(root).items() if not ok]
-    except PatchError:
+    except (PatchError, OSError, ValueError):   # (UnicodeDecodeError is a ValueError) -- a warning's worth
         return None
 
 

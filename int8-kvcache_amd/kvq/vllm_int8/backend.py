@@ -32,6 +32,7 @@ of pairs each (one workgroup per CU streams them in turn) and lengths within 5% 
 Full graphs are offered only for uniform batches the INT8 kernel covers alone (the long-query path sizes
 buffers from host-side lengths).
 """
+import inspect
 import os
 from typing import ClassVar
 
@@ -194,9 +195,7 @@ class Int8StaticBuilder(TritonAttentionMetadataBuilder):
             return None
         if capturing:
             return self.kvq_segm
-        lens = getattr(c, "seq_lens_cpu_upper_bound", None)
-        if lens is None:
-            lens = getattr(c, "seq_lens_cpu", None)
+        lens = _host_seq_lens(c)
         pays = cuda_kernels.split_pays(np.diff(c.query_start_loc_cpu.numpy()), None if lens is None else lens.numpy(),
                                        self.kvq_hkv, self.kvq_fill)
         return self.kvq_segm if pays else None
@@ -217,6 +216,18 @@ class Int8StaticBuilder(TritonAttentionMetadataBuilder):
         md = super().build_for_cudagraph_capture(common_attn_metadata)
         md.kvq_segm = self._split_for(common_attn_metadata, capturing=True)
         return md
+
+
+def _host_seq_lens(c):
+    """Host-side key counts of a batch without a device sync: vLLM's upper bounds when it has them, else
+    seq_lens_cpu if it is stored data (recent vLLM computes seq_lens_cpu on access from the device tensor,
+    a device-to-host copy per step); None (unknown) otherwise."""
+    lens = getattr(c, "seq_lens_cpu_upper_bound", None)
+    if lens is not None:
+        return lens
+    if isinstance(inspect.getattr_static(c, "seq_lens_cpu", None), property):
+        return None
+    return getattr(c, "seq_lens_cpu", None)
 
 
 class Int8StaticImpl(TritonAttentionImpl):

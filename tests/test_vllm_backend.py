@@ -276,6 +276,25 @@ def test_builder_passes_split_buffers_unless_one_pass_serves(tmp_path, monkeypat
     assert b.build_for_cudagraph_capture(_common([1] * n, [4096] * n, upper=even)).kvq_segm is b.kvq_segm
 
 
+def test_host_lengths_never_sync_the_device():
+    """The split rule's host lengths: vLLM's upper bounds, else a stored seq_lens_cpu; a seq_lens_cpu that
+    the metadata computes on access (a device-to-host copy in recent vLLM) is not touched -- the lengths
+    then count as unknown and the split buffers go in."""
+    upper, stored = torch.tensor([5, 6]), torch.tensor([7, 8])
+    assert backend._host_seq_lens(SimpleNamespace(seq_lens_cpu_upper_bound=upper, seq_lens_cpu=stored)) is upper
+    assert backend._host_seq_lens(SimpleNamespace(seq_lens_cpu=stored)) is stored
+    touched = []
+
+    class Computed:
+        seq_lens_cpu_upper_bound = None
+
+        @property
+        def seq_lens_cpu(self):
+            touched.append(1)
+            return stored
+    assert backend._host_seq_lens(Computed()) is None and not touched
+
+
 @pytest.mark.parametrize("spec,level", [(None, "UNIFORM_BATCH"), (7, "UNIFORM_BATCH"), (8, "UNIFORM_SINGLE_TOKEN_DECODE")])
 def test_graph_support_follows_the_verification_length(spec, level):
     cfg = _vllm_config({}, spec_tokens=spec)

@@ -173,3 +173,52 @@ def test_missing_tables_names_what_the_plugin_warns_about(tmp_path):
     vd.install(pkg)
     assert vd.missing_tables(pkg) == []
     assert vd.missing_tables(str(tmp_path)) is None     # not a vLLM source tree: the plugin stays quiet
+
+
+@pytest.mark.parametrize("stage", ["write", "replace"])
+def test_failed_install_leaves_vllm_as_it_was(tmp_path, monkeypatch, stage):
+    """An I/O failure part-way through install() -- writing the second edited file, or moving the second
+    into place after the first was replaced -- leaves all three tables as they were and no temporary
+    files behind, then re-raises."""
+    pkg = make_tree(tmp_path)
+    before = snapshot(pkg)
+    if stage == "write":
+        real_open = open
+        calls = []
+
+        def failing_open(path, mode="r", *a, **k):
+            if str(path).endswith(".kvq-tmp") and "w" in mode:
+                calls.append(path)
+                if len(calls) == 2:
+                    raise OSError(28, "No space left on device")
+            return real_open(path, mode, *a, **k)
+        monkeypatch.setattr("builtins.open", failing_open)
+    else:
+        real_replace = vd._replace
+        done = []
+
+        def failing_replace(src, dst):
+            if done:
+                raise PermissionError(13, "Permission denied", dst)
+            real_replace(src, dst)
+            done.append(dst)
+        monkeypatch.setattr(vd, "_replace", failing_replace)
+    with pytest.raises(OSError):
+        vd.install(pkg)
+    monkeypatch.undo()
+    assert snapshot(pkg) == before
+    leftovers = [f for _, _, fs in os.walk(pkg) for f in fs if f.endswith(".kvq-tmp")]
+    assert leftovers == []
+    assert vd.missing_tables(pkg) == list(vd.FILES.values())
+
+
+def test_missing_tables_stays_quiet_on_unreadable_sources(tmp_path):
+    """missing_tables() is the plugin's warning: an unreadable or undecodable vLLM source is reported as
+    'not a table tree' (None), never raised into vLLM's plugin loading."""
+    pkg = make_tree(tmp_path)
+    with open(os.path.join(pkg, vd.FILES["torch_dtype"]), "wb") as f:
+        f.write(b"\xff\xfe\x00 not utf-8 \x80\x81")
+    assert vd.missing_tables(pkg) is None
+    os.remove(os.path.join(pkg, vd.FILES["torch_dtype"]))
+    os.mkdir(os.path.join(pkg, vd.FILES["torch_dtype"]))    # a directory where the file should be
+    assert vd.missing_tables(pkg) is None
