@@ -356,18 +356,16 @@ def rw_floor(read_bytes, write_bytes, reps=20):
     return best[0] * 1e3, best[1]
 
 
-def bench_c1(reps=20):
-    """Fused quantize + cache write, 16384 tokens x 4 x 128, ~2% padding, 4096 x 16 interleaved cache.
-    4 distinct input/cache sets (~400 MB) are rotated to defeat the 256 MB last-level cache."""
+def _c1_at(T, num_blocks, nsets, reps):
+    """Kernel and scatter-floor time of the fused quantize + cache write for T tokens (c0 distribution,
+    ~2% padding) into num_blocks x 16 interleaved caches, nsets distinct input / cache sets rotated."""
     sets = []
-    for s in range(4):
-        c = synth.c1_inputs(seed=5 + s)
+    for s in range(nsets):
+        c = synth.c1_inputs(seed=5 + s, T=T, num_blocks=num_blocks)
         kv, kc, vc = interleaved_cache(c["num_blocks"], 4, c["block_size"], 128)
         sets.append((c["key"].to(DEV), c["value"].to(DEV), kc, vc, c["slots"].to(DEV),
                      {k: v.to(DEV) for k, v in c["static"].items()}))
-    T = sets[0][0].shape[0]
     t_valid = int((sets[0][4] >= 0).sum())
-    alg = t_valid * 3072 + T * 8 + 6144
 
     def fn(i):
         k, v, kc, vc, sl, st = sets[i]
@@ -384,10 +382,25 @@ def bench_c1(reps=20):
                      torch.cuda.current_stream().cuda_stream)
 
     ms_sc = _median_event_ms(scatter, reps, len(sets))
+    set_bytes = sum(t.numel() * t.element_size() for t in sets[0][:4])
     del sets
+    return ms, ms_sc, t_valid, set_bytes
+
+
+def bench_c1(reps=20):
+    """Fused quantize + cache write, 16384 tokens x 4 x 128, ~2% padding, 4096 x 16 interleaved cache.
+    4 distinct input/cache sets (~400 MB) are rotated to defeat the 256 MB last-level cache. The same at
+    4x the tokens (65,536 into 16,384 x 16 slots, 2 sets, ~390 MB) shows what the kernel sustains once a
+    launch's ramp-up and tail are a smaller share of it."""
+    T = 16384
+    ms, ms_sc, t_valid, _ = _c1_at(T, 4096, 4, reps)
+    alg = t_valid * 3072 + T * 8 + 6144
     # and a plain in-order stream of those bytes (no scatter)
     f_us, f_wg = rw_floor(t_valid * 2048, t_valid * 1024)
     sc_alg = t_valid * 3072
+    T4 = 4 * T
+    ms4, ms4_sc, t4_valid, set4 = _c1_at(T4, 16384, 2, reps)
+    alg4 = t4_valid * 3072 + T4 * 8 + 6144
     return {"us": round(ms * 1e3, 2), "GBps": round(alg / ms / 1e6, 1), "frac": round(alg / ms / 1e6 / PEAK_GBS, 4),
             "alg_bytes": alg, "tokens": T, "valid": t_valid,
             "ceiling": {"us": round(ms_sc * 1e3, 2), "GBps": round(sc_alg / ms_sc / 1e6, 1),
@@ -399,7 +412,14 @@ def bench_c1(reps=20):
             "ceiling_linear": {"us": round(f_us, 2), "GBps": round(sc_alg / f_us / 1e3, 1),
                                "kernel_vs_ceiling": round(ms * 1e3 / f_us, 3),
                                "how": "kvq_stream_rw: %d B read + %d B written in order (no scatter), %d workgroups "
-                                      "per CU" % (t_valid * 2048, t_valid * 1024, f_wg)}}
+                                      "per CU" % (t_valid * 2048, t_valid * 1024, f_wg)},
+            "x4_tokens": {"tokens": T4, "valid": t4_valid, "us": round(ms4 * 1e3, 2),
+                          "GBps": round(alg4 / ms4 / 1e6, 1), "frac": round(alg4 / ms4 / 1e6 / PEAK_GBS, 4),
+                          "ceiling_us": round(ms4_sc * 1e3, 2),
+                          "ceiling_frac_of_peak": round(t4_valid * 3072 / ms4_sc / 1e6 / PEAK_GBS, 4),
+                          "kernel_vs_ceiling": round(ms4 / ms4_sc, 3), "rotated_bytes": 2 * set4,
+                          "how": "the same kernel and scatter floor at 4x c1's tokens, 16,384 x 16 slots, 2 rotated "
+                                 "input / cache sets"}}
 
 
 def bench_c3(reps=20, one_pass=True):

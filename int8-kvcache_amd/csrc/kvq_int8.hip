@@ -363,7 +363,11 @@ __global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC
   // Each thread requests its table entries first, then its wavefront's first tokens, and builds its
   // entries once they (and only they: the loads return in order) have arrived; a barrier on LDS alone
   // then publishes the table while the tokens are still in flight.
-  __shared__ float4 tab[5][CH / 4];  // k_scale, v_scale, k_mu, 1 / k_scale, 1 / v_scale of channels part * CH + c
+  // k_scale, v_scale, k_mu, 1 / k_scale, 1 / v_scale of channels part * CH + c, each table in two halves:
+  // tab[t][0][l] = channels 8 l .. 8 l + 3, tab[t][1][l] = channels 8 l + 4 .. 8 l + 7 -- lane l's two
+  // 16-byte reads of a table are then at lane-contiguous addresses (a [t][2 l], [t][2 l + 1] layout puts
+  // the lanes 32 bytes apart: 218,480 bank-conflict cycles per c1 call)
+  __shared__ float4 tab[5][2][CH / 8];
   constexpr int NTAB = 3 * CH / 4, TPT = (NTAB + QC_ROW_BLOCK - 1) / QC_ROW_BLOCK;
   float tv[TPT][4];
   auto table_loads = [&] {
@@ -387,9 +391,10 @@ __global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC
     for (int j = 0; j < TPT; ++j) {
       const int i = (int)threadIdx.x + j * QC_ROW_BLOCK;
       if (i < NTAB) {
-        const int t = i / (CH / 4);
-        tab[t][i % (CH / 4)] = float4{tv[j][0], tv[j][1], tv[j][2], tv[j][3]};
-        if (t < 2) tab[3 + t][i % (CH / 4)] = float4{1.f / tv[j][0], 1.f / tv[j][1], 1.f / tv[j][2], 1.f / tv[j][3]};
+        const int t = i / (CH / 4), e = i % (CH / 4);   // entry e: channels 4 e .. 4 e + 3
+        tab[t][e & 1][e >> 1] = float4{tv[j][0], tv[j][1], tv[j][2], tv[j][3]};
+        if (t < 2)
+          tab[3 + t][e & 1][e >> 1] = float4{1.f / tv[j][0], 1.f / tv[j][1], 1.f / tv[j][2], 1.f / tv[j][3]};
       }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");   // LDS writes done; token loads stay in flight
@@ -419,9 +424,9 @@ __global__ __launch_bounds__(QC_ROW_BLOCK) __attribute__((amdgpu_waves_per_eu(QC
     vin[j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff, 2 * t * val_st, QC_LOAD_AUX);
     __builtin_amdgcn_sched_barrier(0);
   };
-  const int c4 = lane * (QC_CPL / 4);             // this lane's 8 channels: tab[.][c4], tab[.][c4 + 1]
-  auto tab8 = [&](int t, float (&o)[QC_CPL]) {
-    const float4 a = tab[t][c4], b = tab[t][c4 + 1];
+  static_assert(QC_CPL == 8, "a lane's channels are one entry of each table half");
+  auto tab8 = [&](int t, float (&o)[QC_CPL]) {   // this lane's 8 channels: tab[.][0][lane], tab[.][1][lane]
+    const float4 a = tab[t][0][lane], b = tab[t][1][lane];
     o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
   };
   float kr[QC_CPL], vr[QC_CPL], mu[QC_CPL];
@@ -2013,16 +2018,33 @@ __global__ __launch_bounds__(WAVE * 2 * KS) void verify_kernel(AttnArgs a) {
 // merge needs neither the plan nor any buffer beyond the split buffers of the call.
 constexpr int RED_WAVES = 4;
 constexpr int MERGE_Z = 64;   // largest z extent of split_reduce_kernel's grid
+// pieces of a row fetched together with its denominators (c3: 59.4 -> 59.0 us same box, c4 unchanged;
+// 4 pieces: 61.4 us -- the extra reads of rows with fewer pieces cost more than the round trip saves)
+constexpr int MERGE_SPEC = 2;
 template <int D>
 __device__ __forceinline__ void merge_row(const AttnArgs& a, int tok, int t, int h, int lane) {
   // denominators as the attention kernel left them: piece-0 slot -1 = not cut (already written);
   // otherwise pieces 0..S-2 hold l >= 0 and the last piece -2 - l
   const int64_t base = (int64_t)(tok + t) * a.seg_st + (int64_t)h * a.seg_sh;
-  // the maxima are fetched with the denominators (one memory round trip), and the pieces' partial
-  // outputs four at a time, so a row costs about three round trips whatever its piece count
+  // the maxima and the first MERGE_SPEC pieces' partial outputs are fetched with the denominators (one
+  // memory round trip for a row of up to MERGE_SPEC pieces), later pieces four at a time
   const bool held = lane < a.max_splits;
+  constexpr int CPL = D / WAVE, UNR = 4;
+  const float* po = a.segm_out + base * D + CPL * lane;
   const float enc = held ? a.segm_sum[base + lane] : -1.f;
   const float mraw = held ? a.segm_max[base + lane] : -INFINITY;
+  float v0[MERGE_SPEC][CPL];
+#pragma unroll
+  for (int j = 0; j < MERGE_SPEC; ++j) {  // (in bounds: slots past the buffers' pieces re-read the last)
+    const float* p = po + (int64_t)min(j, a.max_splits - 1) * D;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) v0[j][e] = p[e];
+  }
+  // keep those loads here, ahead of the test below (the compiler would otherwise sink them into it)
+#pragma unroll
+  for (int j = 0; j < MERGE_SPEC; ++j)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) asm volatile("" : "+v"(v0[j][e]));
   const unsigned long long neg = __ballot(enc < 0.f);
   if (neg == 0ull) return;
   const int last = __builtin_ctzll(neg);
@@ -2034,12 +2056,17 @@ __device__ __forceinline__ void merge_row(const AttnArgs& a, int tok, int t, int
   const float wt = lane < S ? __builtin_amdgcn_exp2f(ms - M) : 0.f;
   const float den = wave_sum(wt * ls);
   const float inv = 1.f / __builtin_fmaxf(den, 1e-30f);
-  constexpr int CPL = D / WAVE, UNR = 4;
-  const float* po = a.segm_out + base * D + CPL * lane;
   float num[CPL];
 #pragma unroll
   for (int e = 0; e < CPL; ++e) num[e] = 0.f;
-  for (int s0 = 0; s0 < S; s0 += UNR) {
+#pragma unroll
+  for (int j = 0; j < MERGE_SPEC; ++j) {
+    const bool in = j < S;
+    const float ws = __shfl(wt, min(j, S - 1), WAVE);
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) num[e] = in ? __builtin_fmaf(ws, v0[j][e], num[e]) : num[e];
+  }
+  for (int s0 = MERGE_SPEC; s0 < S; s0 += UNR) {
     float v[UNR][CPL];
 #pragma unroll
     for (int j = 0; j < UNR; ++j) {  // pieces past the last re-read it (in bounds), unused
