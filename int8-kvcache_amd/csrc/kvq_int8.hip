@@ -65,7 +65,7 @@ constexpr int DEFAULT_SEG_COST_LDS_RING = 12;  // the same for the LDS-ring kern
 constexpr int DEFAULT_PREFETCH = 2;
 constexpr int DEFAULT_V32_RING = 2;     // verify_kernel's ring slots (3 with one key split)
 constexpr int DEFAULT_V32_KSPLIT = 2;   // verify_kernel's key splits per workgroup
-constexpr int DEFAULT_SEG_COST_V32_KS2 = 16;  // fixed cost of a segment in verify_kernel with 2 key splits
+constexpr int DEFAULT_SEG_COST_V32_KS2 = 14;  // fixed cost of a segment in verify_kernel with 2 key splits
 constexpr int NUM_XCDS = 8;
 
 // ------------------------------------------------------------------------------------------------
@@ -2805,7 +2805,11 @@ int seg_cost_units(bool lds_ring, int v32_key_splits) {
   }();
   // verify_kernel with 2 key splits streams a unit (one 32-key tile of the segment) in half the time, so
   // its fixed cost is more units (c3, 3-slot rings: 12 -> 24 units 68.5 -> 66.1 us, 36 units 67.3, 48
-  // units 71.3; 2-slot rings: 16 units 65.1-65.3 us, 24 units 66.1-66.9)
+  // units 71.3; 2-slot rings: 16 units 65.1-65.3 us, 24 units 66.1-66.9; with the merge's speculative
+  // loads, same box: 10, 12, 14, 16, 20 units 59.7, 59.3, 58.6, 59.0, 60.3 us -- a piece's measured fixed
+  // cost, prologue + epilogue + the step between pieces, is ~6.5 us, about 10 tiles at 1.35 us per step of
+  // 2 tiles; a little more than that balances best, as the plan's first piece of a worker also waits for
+  // the plan)
   if (env >= 0) return env;
   if (v32_key_splits == 2) return DEFAULT_SEG_COST_V32_KS2;
   return lds_ring ? DEFAULT_SEG_COST_LDS_RING : DEFAULT_SEG_COST;
