@@ -2393,6 +2393,9 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       const char* kr = kb[half] + kro[i];
       const char* vr = vb[half] + vro[i];
       asm volatile("" : "+s"(kr), "+s"(vr));
+      // the lane's offsets, too, are re-declared here: hoisted out of the tile loop as 64-bit values
+      // (a different block), they made every address a 64-bit VGPR addition instead of the saddr form
+      asm volatile("" : "+v"(kvo[i]), "+v"(vvo[i]));
       __builtin_amdgcn_global_load_lds((const void*)(kr + (uint64_t)kvo[i]),
                                        (__attribute__((address_space(3))) void*)(ring[st][0] + 1024 * (IPW * wave + i)), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((const void*)(vr + (uint64_t)vvo[i]),
@@ -2416,6 +2419,16 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   uint32_t kadr[DS];
 #pragma unroll
   for (int s = 0; s < DS; ++s) kadr[s] = ring0 + n * ROWB + 16 * ((4 * s + g) ^ kswz(n));
+  // A ring stage is a run-time int (its byte offset added to the LDS read addresses) or a
+  // std::integral_constant (the offset goes into the reads' immediate field: no VALU per tile).
+  auto stage_vofs = [](auto st_t) -> uint32_t {
+    if constexpr (std::is_same_v<decltype(st_t), int>) return (uint32_t)(st_t * 2 * TILEB);
+    else return 0u;
+  };
+  auto stage_iofs = [](auto st_t) -> int {
+    if constexpr (std::is_same_v<decltype(st_t), int>) return 0;
+    else return decltype(st_t)::value * 2 * TILEB;
+  };
 
   float m[RB], l[RB];
   f32x4 acc[RB][VT];
@@ -2435,16 +2448,15 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // stage), which would empty the ring every tile
   // mask_t: std::false_type = no key of the tile is past any row's limit; true_type = test when the
   // tile reaches the causal edge of some row of the wavefront
-  auto scores = [&](int st, int c, auto mask_t) {
+  auto scores = [&](auto st_t, int c, auto mask_t) {
     pr_prio<1>();
     const int n0 = c * PR_KEYS;
-    const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
     uint32_t ad[DS];
 #pragma unroll
-    for (int s = 0; s < DS; ++s) ad[s] = kadr[s] + so;
+    for (int s = 0; s < DS; ++s) ad[s] = kadr[s] + stage_vofs(st_t);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int KOFS = b * 16 * ROWB;  // key rows 16 + n: same swizzle, 16 rows on
+      const int KOFS = b * 16 * ROWB + stage_iofs(st_t);  // key rows 16 + n: same swizzle, 16 rows on
       bf16x8 kop[DS];
       if constexpr (DS == 4) {
         asm volatile(
@@ -2514,8 +2526,9 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       for (int tt = 0; tt < VT; ++tt) acc[rb][tt] *= alpha;
     }
   };
-  auto softmax_pv = [&](int st) {
-    const uint32_t so = (uint32_t)(st * 2 * TILEB);  // the stage's offset in the ring (uniform)
+  auto softmax_pv = [&](auto st_t) {
+    const uint32_t so = stage_vofs(st_t);
+    const int SOI = stage_iofs(st_t);
     bf16x8 pop[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -2554,7 +2567,8 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
           "ds_read_b64_tr_b16 %7, %11 offset:%c13\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(lo[0]), "=&v"(hi[0]), "=&v"(lo[1]), "=&v"(hi[1]), "=&v"(lo[2]), "=&v"(hi[2]), "=&v"(lo[3]), "=&v"(hi[3])
-          : "v"(vadr[t0] + so), "v"(vadr[t0 + 1] + so), "v"(vadr[t0 + 2] + so), "v"(vadr[t0 + 3] + so), "i"(0), "i"(16 * ROWB)
+          : "v"(vadr[t0] + so), "v"(vadr[t0 + 1] + so), "v"(vadr[t0 + 2] + so), "v"(vadr[t0 + 3] + so), "i"(SOI),
+            "i"(SOI + 16 * ROWB)
           : "memory");
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -2579,6 +2593,16 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       issue(c + NS - 1, snext, lin_t);
       scores(scur, c, mask_t);
     };
+    // the same for tile c in stage ST = c % NS, known at compile time
+    auto next_tile_ct = [&](int c, auto st_t, auto lin_t) {
+      constexpr int ST = decltype(st_t)::value;
+      wait_vm<2 * IPW * (NS - 2)>();
+      lds_barrier();
+      issue(c + NS - 1, (ST + NS - 1) % NS, lin_t);
+      scores(st_t, c, std::false_type{});
+      softmax_pv(st_t);
+      __builtin_amdgcn_sched_barrier(0);  // tiles of a round are not interleaved (register pressure)
+    };
     auto advance = [&]() {
       scur = scur == NS - 1 ? 0 : scur + 1;
       snext = snext == NS - 1 ? 0 : snext + 1;
@@ -2600,6 +2624,14 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       softmax_pv(scur);
       advance();
       int c = 1;
+      // unmasked tiles in rounds of NS, tile c in stage c % NS (1, 2, 0 from c = 1 on)
+      static_assert(NS == 3, "the rounds below are written for a 3-stage ring");
+      for (; c + NS <= J; c += NS) {
+        next_tile_ct(c, std::integral_constant<int, 1>{}, lin_t);
+        next_tile_ct(c + 1, std::integral_constant<int, 2>{}, lin_t);
+        next_tile_ct(c + 2, std::integral_constant<int, 0>{}, lin_t);
+      }
+      // scur / snext still hold the stages of tile c: a round moves c by NS, the ring's period
       for (; c < J; ++c) {
         next_tile(c, lin_t, std::false_type{});
         softmax_pv(scur);
