@@ -2827,9 +2827,10 @@ int log2i(int64_t x) {
   return r;
 }
 // Work units (32-key tiles of one workgroup's streaming) charged per segment for its fixed cost in
-// the stream-K partition, per kernel (KVQ_SEG_COST overrides both)
+// the stream-K partition, per kernel (KVQ_SEG_COST overrides both). Like the other tuning variables,
+// read at every call.
 int seg_cost_units(bool lds_ring, int v32_key_splits) {
-  static const int env = [] {
+  const int env = [] {
     const char* e = getenv("KVQ_SEG_COST");
     if (!e) return -1;
     const int v = atoi(e);
@@ -2849,12 +2850,9 @@ int seg_cost_units(bool lds_ring, int v32_key_splits) {
 
 // slots of the attention's shared LDS ring (KVQ_LDS_PREFETCH: 3, 4 or 6)
 int lds_prefetch_depth() {
-  static const int depth = [] {
-    const char* e = getenv("KVQ_LDS_PREFETCH");
-    const int v = e ? atoi(e) : DEFAULT_LDS_PREFETCH;
-    return v <= 3 ? 3 : (v >= 6 ? 6 : 4);
-  }();
-  return depth;
+  const char* e = getenv("KVQ_LDS_PREFETCH");
+  const int v = e ? atoi(e) : DEFAULT_LDS_PREFETCH;
+  return v <= 3 ? 3 : (v >= 6 ? 6 : 4);
 }
 
 // slots of verify_kernel's LDS ring (KVQ_V32_RING: 2, 3 or 4; 2 only with two key splits, where it is
@@ -2874,12 +2872,9 @@ int v32_key_splits() {
 // Register tiles per wavefront in the attention ring (KVQ_PREFETCH overrides the default; d128 is
 // instantiated for 2, 3, 4, 6, 8 and d64 for 2, 3, 4 -- other values run depth 4).
 int prefetch_depth() {
-  static const int depth = [] {
-    const char* e = getenv("KVQ_PREFETCH");
-    const int v = e ? atoi(e) : DEFAULT_PREFETCH;
-    return v < 2 ? 2 : (v > 8 ? 8 : v);
-  }();
-  return depth;
+  const char* e = getenv("KVQ_PREFETCH");
+  const int v = e ? atoi(e) : DEFAULT_PREFETCH;
+  return v < 2 ? 2 : (v > 8 ? 8 : v);
 }
 
 int device_cus() {
