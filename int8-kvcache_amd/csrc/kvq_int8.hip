@@ -2126,6 +2126,23 @@ __device__ __forceinline__ u32x4 dq8(uint32_t w0, uint32_t w1, const float* s) {
 }
 
 // 8 codes (two dwords) -> 8 bf16 (one 16-byte store)
+// 8 int8 codes -> 8 bf16 (exact: |code| <= 128)
+__device__ __forceinline__ u32x4 cv8(uint32_t w0, uint32_t w1) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  uint32_t r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = j < 2 ? w0 : w1;
+    bf2 h;
+    h.x = (__bf16)i8f(w, 2 * (j & 1));
+    h.y = (__bf16)i8f(w, 2 * (j & 1) + 1);
+    r[j] = *reinterpret_cast<uint32_t*>(&h);
+  }
+  u32x4 o;
+  o.x = r[0]; o.y = r[1]; o.z = r[2]; o.w = r[3];
+  return o;
+}
+
 __device__ __forceinline__ u32x4 dq8x(uint32_t w0, uint32_t w1, const float (&s)[8]) {
   const float tmp[8] = {s[0], s[1], s[2], s[3], s[4], s[5], s[6], s[7]};
   return dq8(w0, w1, tmp);
@@ -2232,6 +2249,11 @@ struct PrefillArgs {
   uint32_t kpage, vpage;  // bytes per page (2 k_sb, 2 v_sb: below 2^32)
   uint32_t krow, vrow;    // bytes per slot (2 k_sn, 2 v_sn: a page's slots span below 2^31 bytes)
   int contig;             // a page is block_size slots (k_sb = block_size k_sn, v likewise)
+  // INT8 pages read directly (prefill_i8_kernel): kc / vc are the int8 caches, the strides and the
+  // page / slot sizes above are bytes, and these are the dequantization scales (per channel when *_pc)
+  const float* ks;
+  const float* vs;
+  int ks_pc, vs_pc;
 };
 
 constexpr int PR_RB = 2;                    // 16-row blocks per wavefront
@@ -2240,6 +2262,7 @@ constexpr int PR_KEYS = 32;                 // keys per tile
 constexpr float PR_SLACK = 8.f;             // log2 headroom of the reference maximum (general loop)
 constexpr float PR_FAST_PSUM_MAX = 0x1p60f;  // largest per-lane denominator the fast pass takes (P <= 2^60)
 constexpr int PR_STAGES = 3;                // LDS ring: tiles in flight + the one computed (3 x 16 KB: 3 workgroups per CU)
+constexpr int PR_I8_STAGES = 2;             // INT8 pages: int8 ring stages (2 x 8 KB at D 128, + 2 bf16 stages)
 // Wave priority over a tile's QK block (K operand reads + MFMAs): a wavefront with matrix work ready
 // issues it ahead of the other wavefronts' softmax VALU on its SIMD, so the MFMA pipe idles less
 // (c4 prefill 7.28-7.37 -> 7.16-7.19 ms, same box, identical output; priority over the PV block as well,
@@ -2265,8 +2288,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2_rne(float a, float b) {
 }
 
 
-template <int D>
-__global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
+// Where the K / V tiles come from: the bf16 temporary cache, or the INT8 pages themselves
+// (prefill_i8_kernel below), converted tile by tile either as dequant_pages converts them (bf16 of
+// code x scale) or as exact bf16 codes with the scales folded into q (K) and the output (V).
+constexpr int PR_SRC_BF16 = 0, PR_SRC_I8 = 1, PR_SRC_I8_FOLD = 2;
+
+template <int D, int SRC>
+__device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
+  constexpr bool I8 = SRC != PR_SRC_BF16;
+  constexpr bool FOLD = SRC == PR_SRC_I8_FOLD;
   constexpr int DS = D / 32;                // 32-channel chunks of the QK contraction
   constexpr int VT = D / 16;                // PV channel tiles
   constexpr int RB = PR_RB;
@@ -2280,7 +2310,18 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   // in distinct bank quads), V by 2 * row % CH (the 4 rows x 2 chunks of a transposing read do)
   auto kswz = [](int row) { return row % CH; };
   auto vswz = [](int row) { return (2 * row) % CH; };
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS][2][TILEB];
+  // I8: the DMA brings a tile's codes into a ring of NS8 int8 stages (rows of D bytes, unswizzled); the
+  // workgroup converts the tile into one of two bf16 stages, laid out as the bf16 ring's stages
+  constexpr int NB = I8 ? 2 : NS;           // bf16 stages
+  constexpr int NS8 = PR_I8_STAGES;
+  constexpr int TILE8B = PR_KEYS * D;       // bytes per int8 K (or V) tile
+  constexpr int PPM = TILE8B / 1024;        // DMA instructions per int8 matrix and tile
+  constexpr int IPW8 = 2 * PPM / 4;         // per wavefront and tile, K and V together
+  constexpr int CPR8 = D / 16;              // 16-byte chunks per int8 key row
+  constexpr int RPI8 = 1024 / D;            // int8 key rows per DMA instruction
+  static_assert(NS8 >= 2 && IPW8 * 4 == 2 * PPM && RPI8 <= 16, "int8 ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NB][2][TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring8[I8 ? NS8 : 1][2][I8 ? TILE8B : 16];
 
   const int kvh = blockIdx.y;
   const int lane = threadIdx.x & (WAVE - 1), wave = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -2318,6 +2359,27 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       qop[rb][s] = *reinterpret_cast<bf16x8*>(&w);
     }
   }
+  // FOLD: q' = bf16(q x k_scale) per channel (lane (n, g) holds channels 32 s + 8 g .. + 7), so that
+  // q' . code = q . (code x k_scale) up to that one rounding
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      float sc[8];
+      if (a.ks_pc) {
+        const float4 f0 = *reinterpret_cast<const float4*>(a.ks + kvh * D + 32 * s + 8 * g);
+        const float4 f1 = *reinterpret_cast<const float4*>(a.ks + kvh * D + 32 * s + 8 * g + 4);
+        sc[0] = f0.x; sc[1] = f0.y; sc[2] = f0.z; sc[3] = f0.w; sc[4] = f1.x; sc[5] = f1.y; sc[6] = f1.z; sc[7] = f1.w;
+      } else {
+        const float v = a.ks[kvh];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc[e] = v;
+      }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qop[rb][s][e] = (__bf16)((float)qop[rb][s][e] * sc[e]);
+    }
+  }
 
   // ---- DMA of tile c into ring stage st: wavefront w's instruction i fills key rows
   // RPI * (IPW * w + i) .. + RPI - 1 of each matrix, lane l the physical chunk l % CH of row l / CH.
@@ -2337,8 +2399,18 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     kro[i] = r0 * a.krow;
     vro[i] = r0 * a.vrow;
   }
-  const char* kh = (const char*)(a.kc + (int64_t)kvh * a.k_sh);
-  const char* vh = (const char*)(a.vc + (int64_t)kvh * a.v_sh);
+  // I8: wavefront w's instruction i is number j = w + 4 i of the tile's 2 PPM: matrix j / PPM (K, V),
+  // key rows RPI8 (j % PPM) .. + RPI8 - 1, lane l the 16-byte chunk l % CPR8 of row l / CPR8, landing
+  // at byte 16 l of the instruction's 1 KB (the int8 stage is row-major, D bytes per row)
+  uint32_t o8[IPW8], r8[IPW8];
+#pragma unroll
+  for (int i = 0; i < IPW8; ++i) {
+    const int j = wave + 4 * i, mat = j / PPM, part = j % PPM;
+    o8[i] = (uint32_t)((lane / CPR8) * (mat ? a.v_sn : a.k_sn) + 16 * (lane % CPR8));
+    r8[i] = (uint32_t)(RPI8 * part % 16) * (mat ? a.vrow : a.krow);
+  }
+  const char* kh = I8 ? (const char*)a.kc + (int64_t)kvh * a.k_sh : (const char*)(a.kc + (int64_t)kvh * a.k_sh);
+  const char* vh = I8 ? (const char*)a.vc + (int64_t)kvh * a.v_sh : (const char*)(a.vc + (int64_t)kvh * a.v_sh);
   // Pages as one run: when the pages the workgroup reads are consecutive ids p_0, p_0 + 1, ... and a
   // page is bs slots (the layout dequant_pages writes), key k is slot p_0 bs + k of the head's cache:
   // the tiles' addresses need no block-table read (checked once, by every wavefront alike).
@@ -2385,6 +2457,19 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       vb[0] = vh + ((uint64_t)(uint32_t)p0 * a.vpage + s0 * a.vrow);
       vb[1] = vh + ((uint64_t)(uint32_t)p1 * a.vpage + s1 * a.vrow);
     }
+    if constexpr (I8) {
+#pragma unroll
+      for (int i = 0; i < IPW8; ++i) {
+        const int j = wave + 4 * i, mat = j / PPM, part = j % PPM;  // uniform
+        const int half = RPI8 * part >= 16;
+        const char* b = (mat ? vb[half] : kb[half]) + r8[i];
+        asm volatile("" : "+s"(b));
+        asm volatile("" : "+v"(o8[i]));
+        __builtin_amdgcn_global_load_lds((const void*)(b + (uint64_t)o8[i]),
+                                         (__attribute__((address_space(3))) void*)(ring8[st][mat] + 1024 * part), 16, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const int half = RPI * (IPW * wave + i) >= 16;  // uniform
@@ -2428,6 +2513,87 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   auto stage_iofs = [](auto st_t) -> int {
     if constexpr (std::is_same_v<decltype(st_t), int>) return 0;
     else return decltype(st_t)::value * 2 * TILEB;
+  };
+
+  // ---- I8: conversion of a tile's codes into a bf16 stage by the whole workgroup. Thread x takes the
+  // 8-channel chunk cc = x % CH of key rows x / CH + CR i (i < NPT), K and V, the 8 channels' scales in
+  // registers; a value is (bf16)(code * scale), as dequant_pages computes it, so the MFMAs see the
+  // operands the two-kernel path gives them. A half-wavefront's 8-byte reads cover 256 contiguous
+  // bytes and a quarter-wavefront's 16-byte writes one bf16 row (its chunks permuted): no bank
+  // conflicts. Rows x / CH and x / CH + CR share their swizzles (CR is a multiple of CH). ----
+  constexpr int CR = 256 / CH;
+  constexpr int NPT = PR_KEYS / CR;  // rows per thread: 2 (D 128) or 1 (D 64)
+  static_assert(CR % CH == 0 && NPT * CR == PR_KEYS, "conversion share");
+  float ksc[8], vsc[8];                // !FOLD: the chunk's scales
+  uint32_t cra = 0, cwk = 0, cwv = 0;  // int8 stage 0 read, bf16 stage 0 writes
+  if constexpr (I8) {
+    const int cc = threadIdx.x % CH, crow = threadIdx.x / CH;
+    auto load_scales = [&](const float* sp, int pc, float (&sc)[8]) {
+      if (pc) {
+        const float4 f0 = *reinterpret_cast<const float4*>(sp + kvh * D + 8 * cc);
+        const float4 f1 = *reinterpret_cast<const float4*>(sp + kvh * D + 8 * cc + 4);
+        sc[0] = f0.x; sc[1] = f0.y; sc[2] = f0.z; sc[3] = f0.w; sc[4] = f1.x; sc[5] = f1.y; sc[6] = f1.z; sc[7] = f1.w;
+      } else {
+        const float v = sp[kvh];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc[e] = v;
+      }
+    };
+    if constexpr (!FOLD) {
+      load_scales(a.ks, a.ks_pc, ksc);
+      load_scales(a.vs, a.vs_pc, vsc);
+    }
+    cra = (uint32_t)(uintptr_t)(&ring8[0][0][0]) + crow * D + 8 * cc;
+    cwk = ring0 + crow * ROWB + 16 * (cc ^ kswz(crow));
+    cwv = ring0 + TILEB + crow * ROWB + 16 * (cc ^ vswz(crow));
+  }
+  auto stage8_vofs = [](auto st_t) -> uint32_t {
+    if constexpr (std::is_same_v<decltype(st_t), int>) return (uint32_t)(st_t * 2 * TILE8B);
+    else return 0u;
+  };
+  auto stage8_iofs = [](auto st_t) -> int {
+    if constexpr (std::is_same_v<decltype(st_t), int>) return 0;
+    else return decltype(st_t)::value * 2 * TILE8B;
+  };
+  // int8 stage s8 -> bf16 stage sb (each a run-time int or a std::integral_constant)
+  auto convert = [&](auto s8_t, auto sb_t) {
+    const uint32_t ra = cra + stage8_vofs(s8_t);
+    const uint32_t wk = cwk + stage_vofs(sb_t), wv = cwv + stage_vofs(sb_t);
+    const int RO = stage8_iofs(s8_t), WO = stage_iofs(sb_t);
+    u32x2 kw[NPT], vw[NPT];
+    if constexpr (NPT == 2) {
+      asm volatile(
+          "ds_read_b64 %0, %4 offset:%c5\n"
+          "ds_read_b64 %1, %4 offset:%c6\n"
+          "ds_read_b64 %2, %4 offset:%c7\n"
+          "ds_read_b64 %3, %4 offset:%c8\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kw[0]), "=&v"(kw[1]), "=&v"(vw[0]), "=&v"(vw[1])
+          : "v"(ra), "i"(RO), "i"(RO + CR * D), "i"(RO + TILE8B), "i"(RO + TILE8B + CR * D)
+          : "memory");
+    } else {
+      static_assert(NPT == 1, "rows per thread");
+      asm volatile(
+          "ds_read_b64 %0, %2 offset:%c3\n"
+          "ds_read_b64 %1, %2 offset:%c4\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kw[0]), "=&v"(vw[0])
+          : "v"(ra), "i"(RO), "i"(RO + TILE8B)
+          : "memory");
+    }
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      u32x4 kb, vb;
+      if constexpr (FOLD) {
+        kb = cv8(kw[i].x, kw[i].y);
+        vb = cv8(vw[i].x, vw[i].y);
+      } else {
+        kb = dq8(kw[i].x, kw[i].y, ksc);
+        vb = dq8(vw[i].x, vw[i].y, vsc);
+      }
+      asm volatile("ds_write_b128 %0, %1 offset:%c2" : : "v"(wk), "v"(kb), "i"(WO + i * CR * ROWB) : "memory");
+      asm volatile("ds_write_b128 %0, %1 offset:%c2" : : "v"(wv), "v"(vb), "i"(WO + i * CR * ROWB) : "memory");
+    }
   };
 
   float m[RB], l[RB];
@@ -2582,30 +2748,73 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
   };
 
   if (ntiles > 0) {
-#pragma unroll
-    for (int j = 0; j < NS - 1; ++j) issue(j, j, linear);
     // ring stages of tile c (scur) and of the tile DMA'd while c is computed (snext = stage of c - 1),
-    // advanced after each tile (no division in the loop)
-    int scur = 0, snext = NS - 1;
+    // advanced after each tile (no division in the loop). I8: scur is tile c's bf16 stage (c % 2), s8
+    // its int8 stage (c % NS8).
+    // the first tiles' DMA; I8: NS8 tiles in flight, tile 0 converted once it has landed
+    auto prologue = [&]() {
+      if constexpr (I8) {
+#pragma unroll
+        for (int j = 0; j < NS8; ++j) issue(j, j, linear);
+        wait_vm<IPW8 * (NS8 - 1)>();
+        lds_barrier();
+        convert(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+      } else {
+#pragma unroll
+        for (int j = 0; j < NS - 1; ++j) issue(j, j, linear);
+      }
+    };
+    prologue();
+    int scur = 0, snext = NS - 1, s8 = 0;
     auto next_tile = [&](int c, auto lin_t, auto mask_t) {
-      wait_vm<2 * IPW * (NS - 2)>();  // this wavefront's share of tile c has landed
-      lds_barrier();                  // everyone's share has; stage (c - 1) % NS is free again
-      issue(c + NS - 1, snext, lin_t);
+      if constexpr (I8) {
+        wait_vm<IPW8 * (NS8 - 2)>();  // this wavefront's share of tile c + 1 has landed
+        lds_barrier();                // everyone's has, tile c is converted, and the other bf16 stage
+                                      // (tile c - 1) and tile c's int8 stage are free again
+        issue(c + NS8, s8, lin_t);
+      } else {
+        wait_vm<2 * IPW * (NS - 2)>();  // this wavefront's share of tile c has landed
+        lds_barrier();                  // everyone's share has; stage (c - 1) % NS is free again
+        issue(c + NS - 1, snext, lin_t);
+      }
       scores(scur, c, mask_t);
     };
-    // the same for tile c in stage ST = c % NS, known at compile time
+    // the same for tile c in stage ST = c % NS (I8: bf16 stage c % 2; the int8 stage too when NS8 is 2,
+    // else it is moved on here), known at compile time
     auto next_tile_ct = [&](int c, auto st_t, auto lin_t) {
       constexpr int ST = decltype(st_t)::value;
-      wait_vm<2 * IPW * (NS - 2)>();
-      lds_barrier();
-      issue(c + NS - 1, (ST + NS - 1) % NS, lin_t);
+      if constexpr (I8) {
+        wait_vm<IPW8 * (NS8 - 2)>();
+        lds_barrier();
+        issue(c + NS8, NS8 == 2 ? ST : s8, lin_t);
+      } else {
+        wait_vm<2 * IPW * (NS - 2)>();
+        lds_barrier();
+        issue(c + NS - 1, (ST + NS - 1) % NS, lin_t);
+      }
       scores(st_t, c, std::false_type{});
       softmax_pv(st_t);
+      if constexpr (I8) {  // tile c + 1 into the other bf16 stage
+        if constexpr (NS8 == 2) {
+          convert(std::integral_constant<int, 1 - ST>{}, std::integral_constant<int, 1 - ST>{});
+        } else {
+          s8 = s8 == NS8 - 1 ? 0 : s8 + 1;
+          convert(s8, std::integral_constant<int, 1 - ST>{});
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);  // tiles of a round are not interleaved (register pressure)
     };
+    // after tile c's softmax and PV (the fewest registers live); I8: tile c + 1 is converted into the
+    // other bf16 stage (free since this tile's barrier; its int8 stage landed before that barrier)
     auto advance = [&]() {
-      scur = scur == NS - 1 ? 0 : scur + 1;
-      snext = snext == NS - 1 ? 0 : snext + 1;
+      if constexpr (I8) {
+        convert(s8 == NS8 - 1 ? 0 : s8 + 1, scur ^ 1);
+        scur ^= 1;
+        s8 = s8 == NS8 - 1 ? 0 : s8 + 1;
+      } else {
+        scur = scur == NS - 1 ? 0 : scur + 1;
+        snext = snext == NS - 1 ? 0 : snext + 1;
+      }
     };
     // Fast pass: tile 0 sets each row's reference maximum (acc is still zero), later tiles only
     // accumulate. P = 2^(s c - m) stays finite and keeps its relative precision as long as no score
@@ -2624,14 +2833,22 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
       softmax_pv(scur);
       advance();
       int c = 1;
-      // unmasked tiles in rounds of NS, tile c in stage c % NS (1, 2, 0 from c = 1 on)
-      static_assert(NS == 3, "the rounds below are written for a 3-stage ring");
-      for (; c + NS <= J; c += NS) {
-        next_tile_ct(c, std::integral_constant<int, 1>{}, lin_t);
-        next_tile_ct(c + 1, std::integral_constant<int, 2>{}, lin_t);
-        next_tile_ct(c + 2, std::integral_constant<int, 0>{}, lin_t);
+      if constexpr (I8) {
+        // unmasked tiles in rounds of 2, tile c in bf16 stage c % 2 (1, 0 from c = 1 on)
+        for (; c + 2 <= J; c += 2) {
+          next_tile_ct(c, std::integral_constant<int, 1>{}, lin_t);
+          next_tile_ct(c + 1, std::integral_constant<int, 0>{}, lin_t);
+        }
+      } else {
+        // unmasked tiles in rounds of NS, tile c in stage c % NS (1, 2, 0 from c = 1 on)
+        static_assert(NS == 3, "the rounds below are written for a 3-stage ring");
+        for (; c + NS <= J; c += NS) {
+          next_tile_ct(c, std::integral_constant<int, 1>{}, lin_t);
+          next_tile_ct(c + 1, std::integral_constant<int, 2>{}, lin_t);
+          next_tile_ct(c + 2, std::integral_constant<int, 0>{}, lin_t);
+        }
       }
-      // scur / snext still hold the stages of tile c: a round moves c by NS, the ring's period
+      // the run-time stages still hold tile c's: a round moves c by the rings' period
       for (; c < J; ++c) {
         next_tile(c, lin_t, std::false_type{});
         softmax_pv(scur);
@@ -2660,10 +2877,10 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int tt = 0; tt < VT; ++tt) acc[rb][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-#pragma unroll
-      for (int j = 0; j < NS - 1; ++j) issue(j, j, linear);
+      prologue();
       scur = 0;
       snext = NS - 1;
+      s8 = 0;
       for (int c = 0; c < ntiles; ++c) {
         next_tile(c, linear, std::true_type{});
         row_top();
@@ -2683,12 +2900,35 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
     uint16_t* orow = a.out + (int64_t)(tok + t[rb]) * a.o_st + (int64_t)hq[rb] * a.o_sh + 4 * g;
 #pragma unroll
     for (int tt = 0; tt < VT; ++tt) {
+      f32x4 o = acc[rb][tt] * inv;
+      if constexpr (FOLD) {  // channels 16 tt + 4 g + i: the V scales, applied to the output
+        if (a.vs_pc) {
+          const float4 f = *reinterpret_cast<const float4*>(a.vs + kvh * D + 16 * tt + 4 * g);
+          o[0] *= f.x; o[1] *= f.y; o[2] *= f.z; o[3] *= f.w;
+        } else {
+          o *= a.vs[kvh];
+        }
+      }
       u32x2 w;
-      w.x = pack_bf16x2_rne(acc[rb][tt][0] * inv, acc[rb][tt][1] * inv);
-      w.y = pack_bf16x2_rne(acc[rb][tt][2] * inv, acc[rb][tt][3] * inv);
+      w.x = pack_bf16x2_rne(o[0], o[1]);
+      w.y = pack_bf16x2_rne(o[2], o[3]);
       *reinterpret_cast<u32x2*>(orow + 16 * tt) = w;
     }
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
+  prefill_body<D, PR_SRC_BF16>(a);
+}
+
+// The same attention reading the INT8 pages themselves, in place of dequant_pages + prefill_kernel:
+// no temporary bf16 cache (2 x 2 bytes per key, channel and kv head of the long requests). Each tile
+// is converted in LDS with dequant_pages' arithmetic, so the output is bit-identical to the two-kernel
+// path's.
+template <int D, int SRC>
+__global__ __launch_bounds__(256, 2) void prefill_i8_kernel(PrefillArgs a) {
+  prefill_body<D, SRC>(a);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2973,6 +3213,66 @@ extern "C" {
 
 const char* kvq_last_error(void) { return g_err.c_str(); }
 
+}  // extern "C"
+
+namespace {
+
+// Shared by the bf16 (dequant_pages' temporary cache) and the INT8 (the pages themselves) prefill:
+// es = bytes per cache element (2 or 1); ks / vs only for the INT8 caches.
+int prefill_launch(const char* nm, int es, const void* q, int64_t q_st, int64_t q_sh, const void* k_cache,
+                   int64_t k_sb, int64_t k_sn, int64_t k_sh, const void* v_cache, int64_t v_sb, int64_t v_sn,
+                   int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads, int64_t head_dim,
+                   void* out, int64_t o_st, int64_t o_sh, const int32_t* cu_seqlens_q, const int32_t* seq_lens,
+                   const int32_t* block_table, int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
+                   const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile, double softmax_scale,
+                   const float* k_scale, int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
+                   void* stream) {
+  if (head_dim != 64 && head_dim != 128) return fail("%s: head_dim must be 64 or 128, got %lld", nm, (long long)head_dim);
+  if (block_size < 16 || !pow2(block_size)) return fail("%s: block_size must be a power of two >= 16", nm);
+  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_kv_heads > 65535)
+    return fail("%s: bad head counts Hq=%lld Hkv=%lld", nm, (long long)num_q_heads, (long long)num_kv_heads);
+  if (num_tiles < 0 || num_tiles > INT32_MAX || num_blocks > INT32_MAX) return fail("%s: bad sizes", nm);
+  if (es == 1 && ((k_scale_cols != 1 && k_scale_cols != head_dim) || (v_scale_cols != 1 && v_scale_cols != head_dim)))
+    return fail("%s: scale columns must be 1 or head_dim", nm);
+  if (num_tiles == 0) { g_err.clear(); return KVQ_OK; }
+  // 16-byte rows: the DMA moves 16-byte chunks (8 bf16 or 16 int8 channels)
+  const int64_t ea = 16 / es;
+  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_st | q_sh | o_st | o_sh) % 8 ||
+      (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % ea)
+    return fail("%s: rows must be 16-byte aligned (base pointers and strides)", nm);
+  if (es == 1 && ((k_scale_cols > 1 && !aligned16(k_scale)) || (v_scale_cols > 1 && !aligned16(v_scale))))
+    return fail("%s: per-channel scale tables must be 16-byte aligned", nm);
+  if (rows_per_tile != PR_ROWS) return fail("%s: work list tiles must be %d rows", nm, PR_ROWS);
+  if (k_sb < 0 || v_sb < 0 || k_sn < 0 || v_sn < 0 || es * k_sb > UINT32_MAX || es * v_sb > UINT32_MAX ||
+      es * block_size * k_sn > INT32_MAX || es * block_size * v_sn > INT32_MAX)
+    return fail("%s: page too large for 32-bit page / slot offsets", nm);
+  PrefillArgs a;
+  a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache; a.out = (uint16_t*)out;
+  a.cu_q = cu_seqlens_q; a.seq_lens = seq_lens; a.block_table = block_table; a.tile_req = tile_req; a.tile_row = tile_row;
+  a.q_st = q_st; a.q_sh = q_sh; a.o_st = o_st; a.o_sh = o_sh;
+  a.k_sb = k_sb; a.k_sn = k_sn; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sn = v_sn; a.v_sh = v_sh; a.bt_stride = bt_stride;
+  a.sm_log2 = (float)(softmax_scale * 1.4426950408889634);
+  a.G = (int)(num_q_heads / num_kv_heads); a.lbs = log2i(block_size); a.num_blocks = (int)num_blocks;
+  a.kpage = (uint32_t)(es * k_sb); a.vpage = (uint32_t)(es * v_sb);
+  a.krow = (uint32_t)(es * k_sn); a.vrow = (uint32_t)(es * v_sn);
+  a.contig = (k_sb == block_size * k_sn && v_sb == block_size * v_sn) ? 1 : 0;
+  a.ks = k_scale; a.vs = v_scale; a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)num_tiles, (unsigned)num_kv_heads);
+  if (es == 1) {
+    if (head_dim == 128) hipLaunchKernelGGL((prefill_i8_kernel<128, PR_SRC_I8>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_i8_kernel<64, PR_SRC_I8>), grid, dim3(256), 0, st, a);
+  } else {
+    if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(256), 0, st, a);
+  }
+  return launched(nm);
+}
+
+}  // namespace
+
+extern "C" {
+
 int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const void* k_cache, int64_t k_sb,
                                 int64_t k_sn, int64_t k_sh, const void* v_cache, int64_t v_sb, int64_t v_sn,
                                 int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
@@ -2981,34 +3281,25 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
                                 int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
                                 const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
                                 double softmax_scale, void* stream) {
-  if (head_dim != 64 && head_dim != 128) return fail("paged_prefill_attention: head_dim must be 64 or 128, got %lld", (long long)head_dim);
-  if (block_size < 16 || !pow2(block_size)) return fail("paged_prefill_attention: block_size must be a power of two >= 16");
-  if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_kv_heads > 65535)
-    return fail("paged_prefill_attention: bad head counts Hq=%lld Hkv=%lld", (long long)num_q_heads, (long long)num_kv_heads);
-  if (num_tiles < 0 || num_tiles > INT32_MAX || num_blocks > INT32_MAX) return fail("paged_prefill_attention: bad sizes");
-  if (num_tiles == 0) { g_err.clear(); return KVQ_OK; }
-  if (!aligned16(q) || !aligned16(out) || !aligned16(k_cache) || !aligned16(v_cache) || (q_st | q_sh | o_st | o_sh) % 8 ||
-      (k_sb | k_sn | k_sh | v_sb | v_sn | v_sh) % 8)
-    return fail("paged_prefill_attention: rows must be 16-byte aligned (base pointers and strides)");
-  if (rows_per_tile != PR_ROWS) return fail("paged_prefill_attention: work list tiles must be %d rows", PR_ROWS);
-  if (k_sb < 0 || v_sb < 0 || k_sn < 0 || v_sn < 0 || 2 * k_sb > UINT32_MAX || 2 * v_sb > UINT32_MAX ||
-      2 * block_size * k_sn > INT32_MAX || 2 * block_size * v_sn > INT32_MAX)
-    return fail("paged_prefill_attention: page too large for 32-bit page / slot offsets");
-  PrefillArgs a;
-  a.q = (const uint16_t*)q; a.kc = (const uint16_t*)k_cache; a.vc = (const uint16_t*)v_cache; a.out = (uint16_t*)out;
-  a.cu_q = cu_seqlens_q; a.seq_lens = seq_lens; a.block_table = block_table; a.tile_req = tile_req; a.tile_row = tile_row;
-  a.q_st = q_st; a.q_sh = q_sh; a.o_st = o_st; a.o_sh = o_sh;
-  a.k_sb = k_sb; a.k_sn = k_sn; a.k_sh = k_sh; a.v_sb = v_sb; a.v_sn = v_sn; a.v_sh = v_sh; a.bt_stride = bt_stride;
-  a.sm_log2 = (float)(softmax_scale * 1.4426950408889634);
-  a.G = (int)(num_q_heads / num_kv_heads); a.lbs = log2i(block_size); a.num_blocks = (int)num_blocks;
-  a.kpage = (uint32_t)(2 * k_sb); a.vpage = (uint32_t)(2 * v_sb);
-  a.krow = (uint32_t)(2 * k_sn); a.vrow = (uint32_t)(2 * v_sn);
-  a.contig = (k_sb == block_size * k_sn && v_sb == block_size * v_sn) ? 1 : 0;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)num_tiles, (unsigned)num_kv_heads);
-  if (head_dim == 128) hipLaunchKernelGGL(prefill_kernel<128>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(prefill_kernel<64>, grid, dim3(256), 0, st, a);
-  return launched("paged_prefill_attention");
+  return prefill_launch("paged_prefill_attention", 2, q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn,
+                        v_sh, num_blocks, block_size, num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q,
+                        seq_lens, block_table, bt_stride, num_q_heads, tile_req, tile_row, num_tiles, rows_per_tile,
+                        softmax_scale, nullptr, 1, nullptr, 1, stream);
+}
+
+int kvq_int8_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
+                               int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
+                               int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                               int64_t head_dim, void* out, int64_t o_st, int64_t o_sh,
+                               const int32_t* cu_seqlens_q, const int32_t* seq_lens, const int32_t* block_table,
+                               int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
+                               const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
+                               double softmax_scale, const float* k_scale, int64_t k_scale_cols,
+                               const float* v_scale, int64_t v_scale_cols, void* stream) {
+  return prefill_launch("int8_prefill_attention", 1, q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn,
+                        v_sh, num_blocks, block_size, num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q,
+                        seq_lens, block_table, bt_stride, num_q_heads, tile_req, tile_row, num_tiles, rows_per_tile,
+                        softmax_scale, k_scale, k_scale_cols, v_scale, v_scale_cols, stream);
 }
 
 int kvq_set_attention_events(void* start, void* stop) {
@@ -3064,7 +3355,7 @@ int kvq_stream_scatter(const void* key, int64_t key_st, int64_t key_sh, const vo
   return launched("stream_scatter");
 }
 
-int kvq_abi_version(void) { return 9; }
+int kvq_abi_version(void) { return 10; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -35,6 +35,9 @@ SIGNATURES = {
     "kvq_paged_prefill_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64,
                                     _i64, _f64, _ptr],
+    "kvq_int8_prefill_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
+                                   _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64,
+                                   _i64, _f64, _ptr, _i64, _ptr, _i64, _ptr],
     "kvq_prefill_rows_per_tile": [],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_stream_read": [_ptr, _i64, _ptr, _i64, _ptr],

@@ -212,6 +212,33 @@ class _Ext:
                      block_table.data_ptr(), block_table.stride(0), q.shape[1], tile_req.data_ptr(),
                      tile_row.data_ptr(), n, self.prefill_rows, float(softmax_scale), _stream(q))
 
+    # the same attention read straight from the INT8 pages, in place of dequant_pages + the call above
+    # (no counterpart in the reference, which always dequantizes first: kvq/cuda_kernels.py:106-131)
+    def int8_prefill_attention(self, q, kc, vc, out, cu_q, seq_lens, block_table, tile_req, tile_row, softmax_scale,
+                               ks, vs):
+        n = tile_req.shape[0]
+        if n == 0:
+            return
+        _check_cuda("int8_prefill_attention", q, kc, vc, out, cu_q, seq_lens, block_table, tile_req, tile_row, ks, vs)
+        _check(q.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and kc.dtype == torch.int8 and
+               vc.dtype == torch.int8, "int8_prefill_attention: q and out must be bf16, the caches int8")
+        _check(kc.dim() == 4 and vc.shape == kc.shape and kc.stride(3) == 1 and vc.stride(3) == 1 and q.stride(2) == 1
+               and out.stride(2) == 1 and out.shape[1:] == q.shape[1:] and q.shape[2] == kc.shape[3],
+               "int8_prefill_attention: unsupported shape/layout")
+        for t, nm in ((cu_q, "cu_seqlens_q"), (seq_lens, "seq_lens"), (block_table, "block_table"),
+                      (tile_req, "tile_req"), (tile_row, "tile_row")):
+            _check(t.dtype == torch.int32, f"int8_prefill_attention: {nm} must be int32")
+        _check(block_table.stride(-1) == 1 and tile_row.shape[0] == n, "int8_prefill_attention: index layout")
+        nb, bs, Hkv, d = kc.shape
+        kcols = _scale_cols(ks, "int8_prefill_attention k_scale", Hkv, d)
+        vcols = _scale_cols(vs, "int8_prefill_attention v_scale", Hkv, d)
+        _native.call("kvq_int8_prefill_attention", q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), kc.stride(0),
+                     kc.stride(1), kc.stride(2), vc.data_ptr(), vc.stride(0), vc.stride(1), vc.stride(2), nb, bs, Hkv,
+                     d, out.data_ptr(), out.stride(0), out.stride(1), cu_q.data_ptr(), seq_lens.data_ptr(),
+                     block_table.data_ptr(), block_table.stride(0), q.shape[1], tile_req.data_ptr(),
+                     tile_row.data_ptr(), n, self.prefill_rows, float(softmax_scale), ks.data_ptr(), kcols,
+                     vs.data_ptr(), vcols, _stream(q))
+
     @property
     def prefill_rows(self):
         """(token, q head) rows per work-list entry of the prefill kernel."""
@@ -400,18 +427,26 @@ def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table
     FlashAttention with block_table = plan.block_table). Only the long requests' rows are written;
     short requests are left to decode_attention. The key counts are read on the device (seq_lens), the
     plan's host lengths only size the temporary cache and order the work. KVQ_DEBUG_DUMP=path saves the
-    prefill call's metadata there first (kvq.debug_dump; the reference's dump, kvq/cuda_kernels.py:123-127)."""
+    prefill call's metadata there first (kvq.debug_dump; the reference's dump, kvq/cuda_kernels.py:123-127).
+    KVQ_PREFILL_DIRECT=1 (read at every call): one kernel reads the INT8 pages itself instead
+    (int8_prefill_attention) -- no temporary cache, bit-identical output."""
     bs, h, d = k_cache.shape[1:]
     _check(bs == plan.block_size, f"block size {bs} != plan block size {plan.block_size}")
-    src_req, src_j, bt_tmp = plan.gpu(q.device)
-    kt = torch.empty(src_req.shape[0], bs, h, d, dtype=q.dtype, device=q.device)
-    vt = torch.empty_like(kt)
-    ext().dequant_pages(k_cache, v_cache, kt, vt, block_table, src_req, src_j, static["k_scale"], static["v_scale"])
     tile_req, tile_row = plan.tiles(q.shape[1] // h, q.device)
+    kt_shape = (plan.src_req.shape[0], bs, h, d)
     if os.environ.get("KVQ_DEBUG_DUMP"):  # the prefill call's metadata, for an offline replay (kvq.debug_dump)
         from . import debug_dump
-        debug_dump.dump_long_call(os.environ["KVQ_DEBUG_DUMP"], q, out, cu_seqlens_q, seq_lens, plan, kt, tile_req,
-                                  tile_row, max_query_len, ext().prefill_rows, softmax_scale)
+        debug_dump.dump_long_call(os.environ["KVQ_DEBUG_DUMP"], q, out, cu_seqlens_q, seq_lens, plan, kt_shape,
+                                  tile_req, tile_row, max_query_len, ext().prefill_rows, softmax_scale)
+    if os.environ.get("KVQ_PREFILL_DIRECT") == "1":
+        # the INT8 pages read directly: no temporary cache, same output bits
+        ext().int8_prefill_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, tile_req,
+                                     tile_row, softmax_scale, static["k_scale"], static["v_scale"])
+        return out
+    src_req, src_j, bt_tmp = plan.gpu(q.device)
+    kt = torch.empty(kt_shape, dtype=q.dtype, device=q.device)
+    vt = torch.empty_like(kt)
+    ext().dequant_pages(k_cache, v_cache, kt, vt, block_table, src_req, src_j, static["k_scale"], static["v_scale"])
     ext().paged_prefill_attention(q, kt, vt, out, cu_seqlens_q, seq_lens, bt_tmp, tile_req, tile_row, softmax_scale)
     return out
 

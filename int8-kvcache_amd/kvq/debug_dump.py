@@ -19,13 +19,15 @@ FIELDS = ("cu_seqlens_q", "seq_lens", "block_table", "src_req", "src_j", "tile_r
 
 def dump_long_call(path, q, out, cu_seqlens_q, seq_lens, plan, kt, tile_req, tile_row, max_query_len, rows_per_tile,
                    softmax_scale):
-    """Save the prefill call of one long_attention step (synchronises the device: a debugging aid)."""
+    """Save the prefill call of one long_attention step (synchronises the device: a debugging aid). kt: the
+    temporary cache or its shape (with KVQ_PREFILL_DIRECT=1 none is made; the replay runs the two-kernel
+    consumer on a temporary cache of that shape)."""
     src_req, src_j, bt = (torch.as_tensor(x) for x in (plan.src_req, plan.src_j, plan.block_table))
     d = {"cu_seqlens_q": cu_seqlens_q.cpu(), "seq_lens": seq_lens.cpu()[:cu_seqlens_q.shape[0] - 1].clone(),
          "block_table": bt.cpu(), "src_req": src_req.cpu(), "src_j": src_j.cpu(), "tile_req": tile_req.cpu(),
          "tile_row": tile_row.cpu(), "max_seqlen_q": int(max_query_len), "max_seqlen_k": int(plan.max_seqlen_k),
          "q_shape": tuple(q.shape), "q_stride": tuple(q.stride()), "out_shape": tuple(out.shape),
-         "out_stride": tuple(out.stride()), "kt_shape": tuple(kt.shape), "block_size": int(plan.block_size),
+         "out_stride": tuple(out.stride()), "kt_shape": tuple(getattr(kt, "shape", kt)), "block_size": int(plan.block_size),
          "rows_per_tile": int(rows_per_tile), "softmax_scale": float(softmax_scale)}
     torch.save(d, path)
     return d

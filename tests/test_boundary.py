@@ -59,6 +59,15 @@ def test_abi_rejects_bad_arguments_before_launch():
     rc = lib.kvq_dequant_pages(nul, 0, 0, 0, nul, 0, 0, 0, 10, 16, 4, 128, nul, nul, nul, 0, nul, nul, 3, nul, 7,
                                nul, 128, nul)
     assert rc == 1 and b"scale columns" in lib.kvq_last_error()
+    # INT8 prefill: scale columns 7; then an int8 slot stride of 8 bytes (the DMA moves 16-byte chunks)
+    p8 = [nul, 0, 0, nul, 0, 128, 0, nul, 0, 128, 0, 64, 16, 4, 128, nul, 0, 0, nul, nul, nul, 0, 28, nul, nul, 1,
+          128, 0.1, nul, 7, nul, 128, nul]
+    assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"scale columns" in lib.kvq_last_error()
+    p8[29], p8[5] = 1, 8
+    assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"16-byte aligned" in lib.kvq_last_error()
+    p8[5] = 128
+    p8[14] = 96
+    assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"head_dim must be 64 or 128" in lib.kvq_last_error()
 
 
 def test_noalloc_rejects_oversized_calls_before_any_device_call():
