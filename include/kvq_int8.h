@@ -171,11 +171,14 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
                                 double softmax_scale, void* stream);
 
 /* The same attention read straight from the INT8 pages, in place of kvq_dequant_pages followed by
- * kvq_paged_prefill_attention -- no temporary bf16 cache; output bit-identical to that pair's. No
- * counterpart in the reference, which always dequantizes first (kvq/cuda_kernels.py:106-131). Caches:
- * int8 [num_blocks, block_size, H, D] views with byte strides (multiples of 16) and block_table the
- * requests' own pages, as kvq_int8_decode_attention takes them; k_scale / v_scale as kvq_dequant_pages
- * takes them (k_scale_cols 1 or head_dim). Work list and rows as kvq_paged_prefill_attention. */
+ * kvq_paged_prefill_attention -- no temporary bf16 cache. No counterpart in the reference, which always
+ * dequantizes first (kvq/cuda_kernels.py:106-131). Caches: int8 [num_blocks, block_size, H, D] views
+ * with byte strides (multiples of 16) and block_table the requests' own pages, as
+ * kvq_int8_decode_attention takes them; k_scale / v_scale as kvq_dequant_pages takes them
+ * (k_scale_cols 1 or head_dim). Work list and rows as kvq_paged_prefill_attention. fold_scales 0: K and
+ * V converted as kvq_dequant_pages converts them, output bit-identical to that pair's; 1: the codes
+ * converted exactly, k_scale folded into q (bf16(q x k_scale)) and v_scale applied to the fp32 output
+ * (faster; not bit-identical). */
 int kvq_int8_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
                                int64_t k_sn, int64_t k_sh, const int8_t* v_cache, int64_t v_sb, int64_t v_sn,
                                int64_t v_sh, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
@@ -184,7 +187,7 @@ int kvq_int8_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const 
                                int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
                                const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
                                double softmax_scale, const float* k_scale, int64_t k_scale_cols,
-                               const float* v_scale, int64_t v_scale_cols, void* stream);
+                               const float* v_scale, int64_t v_scale_cols, int64_t fold_scales, void* stream);
 
 /* Rows per work-list entry of kvq_paged_prefill_attention. No counterpart in the reference. */
 int kvq_prefill_rows_per_tile(void);

@@ -2524,24 +2524,19 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   constexpr int CR = 256 / CH;
   constexpr int NPT = PR_KEYS / CR;  // rows per thread: 2 (D 128) or 1 (D 64)
   static_assert(CR % CH == 0 && NPT * CR == PR_KEYS, "conversion share");
-  float ksc[8], vsc[8];                // !FOLD: the chunk's scales
-  uint32_t cra = 0, cwk = 0, cwv = 0;  // int8 stage 0 read, bf16 stage 0 writes
+  // !FOLD: the kv head's scales in LDS, K then V (a per-head scale repeated), read with the codes
+  // (registers for them would cost the kernel its third workgroup per CU)
+  __shared__ __attribute__((aligned(16))) float scl[I8 && !FOLD ? 2 * D : 4];
+  uint32_t cra = 0, cwk = 0, cwv = 0, csa = 0;  // int8 stage 0 read, bf16 stage 0 writes, scales
   if constexpr (I8) {
     const int cc = threadIdx.x % CH, crow = threadIdx.x / CH;
-    auto load_scales = [&](const float* sp, int pc, float (&sc)[8]) {
-      if (pc) {
-        const float4 f0 = *reinterpret_cast<const float4*>(sp + kvh * D + 8 * cc);
-        const float4 f1 = *reinterpret_cast<const float4*>(sp + kvh * D + 8 * cc + 4);
-        sc[0] = f0.x; sc[1] = f0.y; sc[2] = f0.z; sc[3] = f0.w; sc[4] = f1.x; sc[5] = f1.y; sc[6] = f1.z; sc[7] = f1.w;
-      } else {
-        const float v = sp[kvh];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sc[e] = v;
-      }
-    };
     if constexpr (!FOLD) {
-      load_scales(a.ks, a.ks_pc, ksc);
-      load_scales(a.vs, a.vs_pc, vsc);
+      for (int i = threadIdx.x; i < 2 * D; i += 256) {  // before any DMA; the prologue's barrier publishes it
+        const bool v = i >= D;
+        const float* sp = v ? a.vs : a.ks;
+        scl[i] = (v ? a.vs_pc : a.ks_pc) ? sp[kvh * D + i % D] : sp[kvh];
+      }
+      csa = (uint32_t)(uintptr_t)(&scl[0]) + 32 * cc;
     }
     cra = (uint32_t)(uintptr_t)(&ring8[0][0][0]) + crow * D + 8 * cc;
     cwk = ring0 + crow * ROWB + 16 * (cc ^ kswz(crow));
@@ -2561,7 +2556,37 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     const uint32_t wk = cwk + stage_vofs(sb_t), wv = cwv + stage_vofs(sb_t);
     const int RO = stage8_iofs(s8_t), WO = stage_iofs(sb_t);
     u32x2 kw[NPT], vw[NPT];
-    if constexpr (NPT == 2) {
+    f32x4 sk[2], sv[2];  // !FOLD: the chunk's 8 K and 8 V scales
+    if constexpr (!FOLD && NPT == 2) {
+      asm volatile(
+          "ds_read_b64 %0, %8 offset:%c10\n"
+          "ds_read_b64 %1, %8 offset:%c11\n"
+          "ds_read_b64 %2, %8 offset:%c12\n"
+          "ds_read_b64 %3, %8 offset:%c13\n"
+          "ds_read_b128 %4, %9\n"
+          "ds_read_b128 %5, %9 offset:16\n"
+          "ds_read_b128 %6, %9 offset:%c14\n"
+          "ds_read_b128 %7, %9 offset:%c15\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kw[0]), "=&v"(kw[1]), "=&v"(vw[0]), "=&v"(vw[1]), "=&v"(sk[0]), "=&v"(sk[1]), "=&v"(sv[0]),
+            "=&v"(sv[1])
+          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + CR * D), "i"(RO + TILE8B), "i"(RO + TILE8B + CR * D), "i"(4 * D),
+            "i"(4 * D + 16)
+          : "memory");
+    } else if constexpr (!FOLD) {
+      static_assert(NPT == 1, "rows per thread");
+      asm volatile(
+          "ds_read_b64 %0, %6 offset:%c8\n"
+          "ds_read_b64 %1, %6 offset:%c9\n"
+          "ds_read_b128 %2, %7\n"
+          "ds_read_b128 %3, %7 offset:16\n"
+          "ds_read_b128 %4, %7 offset:%c10\n"
+          "ds_read_b128 %5, %7 offset:%c11\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(kw[0]), "=&v"(vw[0]), "=&v"(sk[0]), "=&v"(sk[1]), "=&v"(sv[0]), "=&v"(sv[1])
+          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + TILE8B), "i"(4 * D), "i"(4 * D + 16)
+          : "memory");
+    } else if constexpr (NPT == 2) {
       asm volatile(
           "ds_read_b64 %0, %4 offset:%c5\n"
           "ds_read_b64 %1, %4 offset:%c6\n"
@@ -2588,8 +2613,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
         kb = cv8(kw[i].x, kw[i].y);
         vb = cv8(vw[i].x, vw[i].y);
       } else {
-        kb = dq8(kw[i].x, kw[i].y, ksc);
-        vb = dq8(vw[i].x, vw[i].y, vsc);
+        float kf[8], vf[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          kf[e] = sk[e / 4][e % 4];
+          vf[e] = sv[e / 4][e % 4];
+        }
+        kb = dq8(kw[i].x, kw[i].y, kf);
+        vb = dq8(vw[i].x, vw[i].y, vf);
       }
       asm volatile("ds_write_b128 %0, %1 offset:%c2" : : "v"(wk), "v"(kb), "i"(WO + i * CR * ROWB) : "memory");
       asm volatile("ds_write_b128 %0, %1 offset:%c2" : : "v"(wv), "v"(vb), "i"(WO + i * CR * ROWB) : "memory");
@@ -2924,10 +2955,11 @@ __global__ __launch_bounds__(256, 3) void prefill_kernel(PrefillArgs a) {
 
 // The same attention reading the INT8 pages themselves, in place of dequant_pages + prefill_kernel:
 // no temporary bf16 cache (2 x 2 bytes per key, channel and kv head of the long requests). Each tile
-// is converted in LDS with dequant_pages' arithmetic, so the output is bit-identical to the two-kernel
-// path's.
+// is converted in LDS. PR_SRC_I8: with dequant_pages' arithmetic, so the output is bit-identical to the
+// two-kernel path's. PR_SRC_I8_FOLD: codes converted exactly, k_scale folded into q and v_scale applied
+// to the output (one rounding of q x k_scale in place of one of code x scale per K and V element).
 template <int D, int SRC>
-__global__ __launch_bounds__(256, 2) void prefill_i8_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, 3) void prefill_i8_kernel(PrefillArgs a) {
   prefill_body<D, SRC>(a);
 }
 
@@ -3226,7 +3258,7 @@ int prefill_launch(const char* nm, int es, const void* q, int64_t q_st, int64_t 
                    const int32_t* block_table, int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
                    const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile, double softmax_scale,
                    const float* k_scale, int64_t k_scale_cols, const float* v_scale, int64_t v_scale_cols,
-                   void* stream) {
+                   int64_t fold_scales, void* stream) {
   if (head_dim != 64 && head_dim != 128) return fail("%s: head_dim must be 64 or 128, got %lld", nm, (long long)head_dim);
   if (block_size < 16 || !pow2(block_size)) return fail("%s: block_size must be a power of two >= 16", nm);
   if (num_kv_heads <= 0 || num_q_heads <= 0 || num_q_heads % num_kv_heads || num_kv_heads > 65535)
@@ -3259,7 +3291,10 @@ int prefill_launch(const char* nm, int es, const void* q, int64_t q_st, int64_t 
   a.ks = k_scale; a.vs = v_scale; a.ks_pc = k_scale_cols > 1; a.vs_pc = v_scale_cols > 1;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)num_tiles, (unsigned)num_kv_heads);
-  if (es == 1) {
+  if (es == 1 && fold_scales) {
+    if (head_dim == 128) hipLaunchKernelGGL((prefill_i8_kernel<128, PR_SRC_I8_FOLD>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((prefill_i8_kernel<64, PR_SRC_I8_FOLD>), grid, dim3(256), 0, st, a);
+  } else if (es == 1) {
     if (head_dim == 128) hipLaunchKernelGGL((prefill_i8_kernel<128, PR_SRC_I8>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((prefill_i8_kernel<64, PR_SRC_I8>), grid, dim3(256), 0, st, a);
   } else {
@@ -3284,7 +3319,7 @@ int kvq_paged_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const
   return prefill_launch("paged_prefill_attention", 2, q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn,
                         v_sh, num_blocks, block_size, num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q,
                         seq_lens, block_table, bt_stride, num_q_heads, tile_req, tile_row, num_tiles, rows_per_tile,
-                        softmax_scale, nullptr, 1, nullptr, 1, stream);
+                        softmax_scale, nullptr, 1, nullptr, 1, 0, stream);
 }
 
 int kvq_int8_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const int8_t* k_cache, int64_t k_sb,
@@ -3295,11 +3330,12 @@ int kvq_int8_prefill_attention(const void* q, int64_t q_st, int64_t q_sh, const 
                                int64_t bt_stride, int64_t num_q_heads, const int32_t* tile_req,
                                const int32_t* tile_row, int64_t num_tiles, int64_t rows_per_tile,
                                double softmax_scale, const float* k_scale, int64_t k_scale_cols,
-                               const float* v_scale, int64_t v_scale_cols, void* stream) {
+                               const float* v_scale, int64_t v_scale_cols, int64_t fold_scales, void* stream) {
+  if (fold_scales != 0 && fold_scales != 1) return fail("int8_prefill_attention: fold_scales must be 0 or 1");
   return prefill_launch("int8_prefill_attention", 1, q, q_st, q_sh, k_cache, k_sb, k_sn, k_sh, v_cache, v_sb, v_sn,
                         v_sh, num_blocks, block_size, num_kv_heads, head_dim, out, o_st, o_sh, cu_seqlens_q,
                         seq_lens, block_table, bt_stride, num_q_heads, tile_req, tile_row, num_tiles, rows_per_tile,
-                        softmax_scale, k_scale, k_scale_cols, v_scale, v_scale_cols, stream);
+                        softmax_scale, k_scale, k_scale_cols, v_scale, v_scale_cols, fold_scales, stream);
 }
 
 int kvq_set_attention_events(void* start, void* stop) {

@@ -37,7 +37,7 @@ SIGNATURES = {
                                     _i64, _f64, _ptr],
     "kvq_int8_prefill_attention": [_ptr, _i64, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _i64, _i64, _i64,
                                    _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr, _i64,
-                                   _i64, _f64, _ptr, _i64, _ptr, _i64, _ptr],
+                                   _i64, _f64, _ptr, _i64, _ptr, _i64, _i64, _ptr],
     "kvq_prefill_rows_per_tile": [],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_stream_read": [_ptr, _i64, _ptr, _i64, _ptr],

@@ -213,9 +213,10 @@ class _Ext:
                      tile_row.data_ptr(), n, self.prefill_rows, float(softmax_scale), _stream(q))
 
     # the same attention read straight from the INT8 pages, in place of dequant_pages + the call above
-    # (no counterpart in the reference, which always dequantizes first: kvq/cuda_kernels.py:106-131)
+    # (no counterpart in the reference, which always dequantizes first: kvq/cuda_kernels.py:106-131).
+    # fold=False: bit-identical to that pair; True: scales folded into q and the output (faster)
     def int8_prefill_attention(self, q, kc, vc, out, cu_q, seq_lens, block_table, tile_req, tile_row, softmax_scale,
-                               ks, vs):
+                               ks, vs, fold=False):
         n = tile_req.shape[0]
         if n == 0:
             return
@@ -237,7 +238,7 @@ class _Ext:
                      d, out.data_ptr(), out.stride(0), out.stride(1), cu_q.data_ptr(), seq_lens.data_ptr(),
                      block_table.data_ptr(), block_table.stride(0), q.shape[1], tile_req.data_ptr(),
                      tile_row.data_ptr(), n, self.prefill_rows, float(softmax_scale), ks.data_ptr(), kcols,
-                     vs.data_ptr(), vcols, _stream(q))
+                     vs.data_ptr(), vcols, int(bool(fold)), _stream(q))
 
     @property
     def prefill_rows(self):
@@ -428,8 +429,9 @@ def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table
     short requests are left to decode_attention. The key counts are read on the device (seq_lens), the
     plan's host lengths only size the temporary cache and order the work. KVQ_DEBUG_DUMP=path saves the
     prefill call's metadata there first (kvq.debug_dump; the reference's dump, kvq/cuda_kernels.py:123-127).
-    KVQ_PREFILL_DIRECT=1 (read at every call): one kernel reads the INT8 pages itself instead
-    (int8_prefill_attention) -- no temporary cache, bit-identical output."""
+    KVQ_PREFILL_DIRECT (read at every call): 1 = one kernel reads the INT8 pages itself instead
+    (int8_prefill_attention) -- no temporary cache, bit-identical output; fold = the same with the scales
+    folded into q and the output (faster, not bit-identical); 0 (default) = the two kernels."""
     bs, h, d = k_cache.shape[1:]
     _check(bs == plan.block_size, f"block size {bs} != plan block size {plan.block_size}")
     tile_req, tile_row = plan.tiles(q.shape[1] // h, q.device)
@@ -438,11 +440,13 @@ def long_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table
         from . import debug_dump
         debug_dump.dump_long_call(os.environ["KVQ_DEBUG_DUMP"], q, out, cu_seqlens_q, seq_lens, plan, kt_shape,
                                   tile_req, tile_row, max_query_len, ext().prefill_rows, softmax_scale)
-    if os.environ.get("KVQ_PREFILL_DIRECT") == "1":
-        # the INT8 pages read directly: no temporary cache, same output bits
+    direct = os.environ.get("KVQ_PREFILL_DIRECT", "0")
+    if direct in ("1", "fold"):
+        # the INT8 pages read directly: no temporary cache ("1": same output bits; "fold": scales folded)
         ext().int8_prefill_attention(q, k_cache, v_cache, out, cu_seqlens_q, seq_lens, block_table, tile_req,
-                                     tile_row, softmax_scale, static["k_scale"], static["v_scale"])
+                                     tile_row, softmax_scale, static["k_scale"], static["v_scale"], direct == "fold")
         return out
+    _check(direct == "0", f"KVQ_PREFILL_DIRECT must be 0, 1 or fold, got {direct!r}")
     src_req, src_j, bt_tmp = plan.gpu(q.device)
     kt = torch.empty(kt_shape, dtype=q.dtype, device=q.device)
     vt = torch.empty_like(kt)

@@ -61,13 +61,15 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert rc == 1 and b"scale columns" in lib.kvq_last_error()
     # INT8 prefill: scale columns 7; then an int8 slot stride of 8 bytes (the DMA moves 16-byte chunks)
     p8 = [nul, 0, 0, nul, 0, 128, 0, nul, 0, 128, 0, 64, 16, 4, 128, nul, 0, 0, nul, nul, nul, 0, 28, nul, nul, 1,
-          128, 0.1, nul, 7, nul, 128, nul]
+          128, 0.1, nul, 7, nul, 128, 0, nul]
     assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"scale columns" in lib.kvq_last_error()
     p8[29], p8[5] = 1, 8
     assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"16-byte aligned" in lib.kvq_last_error()
     p8[5] = 128
     p8[14] = 96
     assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"head_dim must be 64 or 128" in lib.kvq_last_error()
+    p8[14], p8[32] = 128, 2
+    assert lib.kvq_int8_prefill_attention(*p8) == 1 and b"fold_scales must be 0 or 1" in lib.kvq_last_error()
 
 
 def test_noalloc_rejects_oversized_calls_before_any_device_call():
@@ -134,6 +136,18 @@ def test_python_api_shape_checks():
     with pytest.raises(RuntimeError, match="on the GPU"):   # CPU tensors never reach the library
         ck.decode_attention(q, kc16, kc16, q.clone(), cu, cu[1:], torch.zeros(3, 4, dtype=torch.int32), 0.1, st,
                             segm=(torch.zeros(3, 28, 2, 64), torch.zeros(3, 28, 2), torch.zeros(3, 28, 2)))
+
+
+def test_prefill_direct_switch_is_checked(monkeypatch):
+    """KVQ_PREFILL_DIRECT takes 0, 1 or fold; anything else is an error before any launch."""
+    monkeypatch.setenv("KVQ_PREFILL_DIRECT", "yes")
+    q = torch.zeros(40, 28, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(8, 16, 4, 128, dtype=torch.int8)
+    st = {"k_scale": torch.ones(4, 128), "v_scale": torch.ones(4, 128), "k_mu": torch.zeros(4, 128)}
+    cu, sl = torch.tensor([0, 40], dtype=torch.int32), torch.tensor([40], dtype=torch.int32)
+    plan = ck.plan_long(cu, sl, 16)
+    with pytest.raises(RuntimeError, match="KVQ_PREFILL_DIRECT must be 0, 1 or fold"):
+        ck.long_attention(q, kc, kc, q.clone(), cu, sl, torch.arange(3, dtype=torch.int32)[None], 40, plan, 0.1, st)
 
 
 def test_empty_batches_return_early():
