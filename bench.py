@@ -506,6 +506,11 @@ def bench_c4(reps=10, one_pass=True):
                                                                         d ** -0.5), max(3, reps // 2), 1, calls=3)
     pf_flop = sum(L * (L + 1) // 2 for L in pre) * hq * d * 4
     del kt_p, vt_p
+    # the same attention reading the INT8 pages itself (KVQ_PREFILL_DIRECT=1, bit-identical; =fold, scales
+    # folded into q and the output): one kernel in place of dequant_pages + the one above
+    ms_pf8, ms_pf8f = (_median_event_ms(lambda i: ck.ext().int8_prefill_attention(
+        qp, kc, vc, op, cu_pd, sl_pd, bt[96:], tr, tw, d ** -0.5, st["k_scale"], st["v_scale"], fold),
+        max(3, reps // 2), 1, calls=3) for fold in (False, True))
     dq_read = P * bs * hkv * d * 2
     f_us, f_wg = rw_floor(dq_read, 2 * dq_read, reps=reps)
     dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
@@ -521,7 +526,9 @@ def bench_c4(reps=10, one_pass=True):
                                        "bf16 values, no page gather, no arithmetic), %d workgroups per CU"
                                        % (dq_read, 2 * dq_read, f_wg)},
             "prefill_ms": round(ms_pf, 3), "prefill_TFLOPs": round(pf_flop / ms_pf / 1e9, 1),
-            "prefill_frac_bf16": round(pf_flop / ms_pf / 1e9 / PEAK_BF16_TFLOPS, 4), "prefill_flop": pf_flop}
+            "prefill_frac_bf16": round(pf_flop / ms_pf / 1e9 / PEAK_BF16_TFLOPS, 4), "prefill_flop": pf_flop,
+            "prefill_direct_ms": round(ms_pf8, 3), "prefill_fold_ms": round(ms_pf8f, 3),
+            "prefill_two_kernel_ms": round(ms_dq + ms_pf, 3)}
 
 
 def main():

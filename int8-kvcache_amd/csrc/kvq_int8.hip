@@ -2525,7 +2525,9 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
   constexpr int NPT = PR_KEYS / CR;  // rows per thread: 2 (D 128) or 1 (D 64)
   static_assert(CR % CH == 0 && NPT * CR == PR_KEYS, "conversion share");
   // !FOLD: the kv head's scales in LDS, K then V (a per-head scale repeated), read with the codes
-  // (registers for them would cost the kernel its third workgroup per CU)
+  // (registers for them would cost the kernel its third workgroup per CU). Channel 8 c + 4 h + e sits
+  // at float (D / 2) h + 4 c + e of its matrix's D: a quarter-wavefront's 16-byte reads of the first
+  // (or second) four scales of 16 chunks are 256 contiguous bytes (no bank conflicts).
   __shared__ __attribute__((aligned(16))) float scl[I8 && !FOLD ? 2 * D : 4];
   uint32_t cra = 0, cwk = 0, cwv = 0, csa = 0;  // int8 stage 0 read, bf16 stage 0 writes, scales
   if constexpr (I8) {
@@ -2533,10 +2535,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
     if constexpr (!FOLD) {
       for (int i = threadIdx.x; i < 2 * D; i += 256) {  // before any DMA; the prologue's barrier publishes it
         const bool v = i >= D;
+        const int ch = i % D;
         const float* sp = v ? a.vs : a.ks;
-        scl[i] = (v ? a.vs_pc : a.ks_pc) ? sp[kvh * D + i % D] : sp[kvh];
+        scl[(v ? D : 0) + (D / 2) * ((ch >> 2) & 1) + 4 * (ch >> 3) + (ch & 3)] =
+            (v ? a.vs_pc : a.ks_pc) ? sp[kvh * D + ch] : sp[kvh];
       }
-      csa = (uint32_t)(uintptr_t)(&scl[0]) + 32 * cc;
+      csa = (uint32_t)(uintptr_t)(&scl[0]) + 16 * cc;
     }
     cra = (uint32_t)(uintptr_t)(&ring8[0][0][0]) + crow * D + 8 * cc;
     cwk = ring0 + crow * ROWB + 16 * (cc ^ kswz(crow));
@@ -2564,14 +2568,14 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
           "ds_read_b64 %2, %8 offset:%c12\n"
           "ds_read_b64 %3, %8 offset:%c13\n"
           "ds_read_b128 %4, %9\n"
-          "ds_read_b128 %5, %9 offset:16\n"
-          "ds_read_b128 %6, %9 offset:%c14\n"
-          "ds_read_b128 %7, %9 offset:%c15\n"
+          "ds_read_b128 %5, %9 offset:%c14\n"
+          "ds_read_b128 %6, %9 offset:%c15\n"
+          "ds_read_b128 %7, %9 offset:%c16\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(kw[0]), "=&v"(kw[1]), "=&v"(vw[0]), "=&v"(vw[1]), "=&v"(sk[0]), "=&v"(sk[1]), "=&v"(sv[0]),
             "=&v"(sv[1])
-          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + CR * D), "i"(RO + TILE8B), "i"(RO + TILE8B + CR * D), "i"(4 * D),
-            "i"(4 * D + 16)
+          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + CR * D), "i"(RO + TILE8B), "i"(RO + TILE8B + CR * D), "i"(2 * D),
+            "i"(4 * D), "i"(6 * D)
           : "memory");
     } else if constexpr (!FOLD) {
       static_assert(NPT == 1, "rows per thread");
@@ -2579,12 +2583,12 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs& a) {
           "ds_read_b64 %0, %6 offset:%c8\n"
           "ds_read_b64 %1, %6 offset:%c9\n"
           "ds_read_b128 %2, %7\n"
-          "ds_read_b128 %3, %7 offset:16\n"
-          "ds_read_b128 %4, %7 offset:%c10\n"
-          "ds_read_b128 %5, %7 offset:%c11\n"
+          "ds_read_b128 %3, %7 offset:%c10\n"
+          "ds_read_b128 %4, %7 offset:%c11\n"
+          "ds_read_b128 %5, %7 offset:%c12\n"
           "s_waitcnt lgkmcnt(0)"
           : "=&v"(kw[0]), "=&v"(vw[0]), "=&v"(sk[0]), "=&v"(sk[1]), "=&v"(sv[0]), "=&v"(sv[1])
-          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + TILE8B), "i"(4 * D), "i"(4 * D + 16)
+          : "v"(ra), "v"(csa), "i"(RO), "i"(RO + TILE8B), "i"(2 * D), "i"(4 * D), "i"(6 * D)
           : "memory");
     } else if constexpr (NPT == 2) {
       asm volatile(
