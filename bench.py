@@ -182,6 +182,22 @@ def read_ceiling(buf, reps=10):
     return best
 
 
+def mfma_ceiling(reps=5):
+    """TFLOP/s of back-to-back dense bf16 MFMAs (the library's kvq_mfma_probe: 16x16x32, the prefill
+    kernel's instruction) on random bf16 operands, 8 workgroups of 4 wavefronts per CU, ~7 ms per launch,
+    timed as the prefill kernel is (graph replays of 3 calls): the rate the box delivers under its power
+    limit over such a burst, the ceiling beside the prefill kernel's rate."""
+    g = torch.Generator(device=DEV).manual_seed(11)
+    data = torch.randn(8192, generator=g, device=DEV).to(torch.bfloat16)
+    wg = torch.cuda.get_device_properties(0).multi_processor_count * 8
+    out = torch.empty(wg * 256, dtype=torch.float32, device=DEV)
+    iters = 12288
+    stream = torch.cuda.current_stream
+    ms = _median_event_ms(lambda i: _native.call("kvq_mfma_probe", data.data_ptr(), iters, out.data_ptr(), wg,
+                                                 stream().cuda_stream), reps, 1, calls=3)
+    return wg * 4 * iters * 8 * 16384 / ms / 1e9, wg
+
+
 # ------------------------------------------------------------------------------------------------ CPU baseline
 def cpu_baseline(w, out, budget_s=12.0, max_reqs=128):
     """The CPU oracle (port of int8_ref B + run_paged) on whole c2 requests until ~budget_s of CPU work;
@@ -515,6 +531,7 @@ def bench_c4(reps=10, one_pass=True):
     f_us, f_wg = rw_floor(dq_read, 2 * dq_read, reps=reps)
     dec_alg = sum(lens) * hkv * d * 2 + 2 * q.numel() * 2 + sum(dec_pages) * 4
     dq_alg = P * bs * hkv * d * 2 * (1 + 2) + P * 12
+    mfma_tf, mfma_wg = mfma_ceiling(max(3, reps // 2))
     return {"decode_us": round(ms_dec * 1e3, 2), "decode_GBps": round(dec_alg / ms_dec / 1e6, 1),
             "decode_frac": round(dec_alg / ms_dec / 1e6 / PEAK_GBS, 4), "decode_one_pass_us": round(ms_dec1 * 1e3, 2),
             "dequant_us": round(ms_dq * 1e3, 2), "dequant_GBps": round(dq_alg / ms_dq / 1e6, 1),
@@ -528,7 +545,11 @@ def bench_c4(reps=10, one_pass=True):
             "prefill_ms": round(ms_pf, 3), "prefill_TFLOPs": round(pf_flop / ms_pf / 1e9, 1),
             "prefill_frac_bf16": round(pf_flop / ms_pf / 1e9 / PEAK_BF16_TFLOPS, 4), "prefill_flop": pf_flop,
             "prefill_direct_ms": round(ms_pf8, 3), "prefill_fold_ms": round(ms_pf8f, 3),
-            "prefill_two_kernel_ms": round(ms_dq + ms_pf, 3)}
+            "prefill_two_kernel_ms": round(ms_dq + ms_pf, 3),
+            "mfma_ceiling": {"TFLOPs": round(mfma_tf, 1), "frac_of_peak": round(mfma_tf / PEAK_BF16_TFLOPS, 4),
+                             "prefill_vs_ceiling": round(pf_flop / ms_pf / 1e9 / mfma_tf, 4),
+                             "how": "kvq_mfma_probe: back-to-back 16x16x32 bf16 MFMAs on random bf16 operands, "
+                                    "8 chains per wavefront, %d workgroups of 4 wavefronts" % mfma_wg}}
 
 
 def main():

@@ -205,6 +205,13 @@ int kvq_set_attention_events(void* start, void* stop);
  * kernel. Stream-ordered, allocates nothing. */
 int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t workgroups, void* stream);
 
+/* Dense-bf16 MFMA probe, no counterpart in the reference: `workgroups` x 4 wavefronts each run 8
+ * independent chains of 16x16x32 bf16 MFMAs for `iters` rounds (a multiple of 4) on operands from `data`
+ * (16 KB of bf16, 16-byte aligned), storing one float per thread in `out` (workgroups x 256). FLOP per
+ * launch: workgroups x 4 x iters x 8 x 16,384. bench.py times it for the bf16 rate the box sustains
+ * under its power limit, the ceiling beside the prefill kernel's. */
+int kvq_mfma_probe(const void* data, int64_t iters, float* out, int64_t workgroups, void* stream);
+
 /* Instrumentation, no counterpart in the reference: reads `read_bytes` at `src` and writes `write_bytes`
  * at `dst` once, in order, with `workgroups` workgroups of 256 lanes (each a contiguous share of both,
  * the two streams interleaved in the fixed ratio of their sizes; non-temporal loads and stores; the

@@ -2968,6 +2968,37 @@ __global__ __launch_bounds__(256, 3) void prefill_i8_kernel(PrefillArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Dense-bf16 MFMA probe (instrumentation, no counterpart in the reference): every wavefront runs 8
+// independent accumulation chains of v_mfma_f32_16x16x32_bf16 (the prefill kernel's instruction) for
+// `iters` rounds, on operands taken from `data` (1,024 16-byte vectors) and rotated every round, so the
+// multipliers see changing values as the prefill's do; each lane stores a sum of its accumulators (no
+// MFMA is dropped). What it sustains is the dense bf16 rate the box delivers, at the clock its power
+// limit allows for such operands: the ceiling the prefill kernel is compared with.
+__global__ __launch_bounds__(256) void mfma_probe_kernel(const bf16x8* __restrict__ data, int iters,
+                                                         float* __restrict__ out) {
+  const int t = threadIdx.x;
+  bf16x8 x[4], y[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[i] = data[(t * 8 + i) & 1023];
+    y[i] = data[(t * 8 + 4 + i + blockIdx.x) & 1023];
+  }
+  f32x4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int it = 0; it < iters; it += 4) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[j & 3], y[(j + u) & 3], acc[j], 0, 0, 0);
+  }
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) sum += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+  out[(int64_t)blockIdx.x * 256 + t] = sum;
+}
+
+// ------------------------------------------------------------------------------------------------
 // Streaming-read probe (instrumentation, no counterpart in the reference): reads n16 16-byte words
 // once and stores each lane's XOR of what it read (so no load is dropped). Workgroup b streams the
 // b-th contiguous share of the buffer, its wavefronts taking interleaved 1 KB blocks of it with 8
@@ -3348,6 +3379,15 @@ int kvq_set_attention_events(void* start, void* stop) {
   return KVQ_OK;
 }
 
+int kvq_mfma_probe(const void* data, int64_t iters, float* out, int64_t workgroups, void* stream) {
+  if (!data || !out || !aligned16(data) || iters < 4 || iters % 4 || iters > INT32_MAX || workgroups < 1 ||
+      workgroups > INT32_MAX / 256)
+    return fail("mfma_probe: need 16 KB of 16-byte aligned bf16 data, iters a positive multiple of 4, 1..2^23 workgroups");
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3((unsigned)workgroups), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const bf16x8*>(data), (int)iters, out);
+  return launched("mfma_probe");
+}
+
 int kvq_stream_read(const void* data, int64_t bytes, uint32_t* out, int64_t workgroups, void* stream) {
   if (!data || !out || bytes < 16 || bytes % 16 || !aligned16(data) || workgroups < 1 || workgroups > INT32_MAX / 256)
     return fail("stream_read: need a 16-byte aligned buffer of a positive multiple of 16 bytes and 1..2^23 workgroups");
@@ -3395,7 +3435,7 @@ int kvq_stream_scatter(const void* key, int64_t key_st, int64_t key_sh, const vo
   return launched("stream_scatter");
 }
 
-int kvq_abi_version(void) { return 10; }
+int kvq_abi_version(void) { return 11; }
 
 int kvq_prefill_rows_per_tile(void) { return PR_ROWS; }
 

@@ -8,7 +8,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libkvq_int8.so")
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _i64 = ctypes.c_int64
 _ptr = ctypes.c_void_p
@@ -41,6 +41,7 @@ SIGNATURES = {
     "kvq_prefill_rows_per_tile": [],
     "kvq_set_attention_events": [_ptr, _ptr],
     "kvq_stream_read": [_ptr, _i64, _ptr, _i64, _ptr],
+    "kvq_mfma_probe": [_ptr, _i64, _ptr, _i64, _ptr],
     "kvq_stream_rw": [_ptr, _i64, _ptr, _i64, _i64, _ptr],
     "kvq_stream_scatter": [_ptr, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64,
                            _i64, _i64, _i64, _ptr],
